@@ -1,0 +1,212 @@
+"""Benchmark of the EXL3 hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload: the dense 27B-class decoder layer set at K = 3 bpw, MCG codebook, seeded random
+packed codes and +-1 sign vectors: q/k/v 5120 -> 6144+1024+1024 (one fused 3-shard group), o_proj 6144 -> 5120,
+gate/up 5120 -> 17408+17408 (one fused 2-shard group), down 17408 -> 5120, fp16 activations N(0,1) at M = 1.
+One step = the four fused linears (decode-GEMV + rotations) over one batch of M rows.  Inputs are resident in HBM
+before timing starts; R rotating copies of the layer set (>= 512 MB, twice the 256 MB MALL) keep the weights cold.
+
+Prints one JSON line: metric/value = algorithmic HBM GB/s of the layer set at M = 1 (trellis + sign vectors +
+activations in/out, BASELINE.md C2 = 128,174,080 B per step), plus the roofline of the dominant kernel (the fused
+decode-GEMV), the CPU baseline (the numpy oracle, 1 core, on a bounded sample), the M = 4 / 16 rates and the prefill
+decode-GEMM rate when that path is present.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+LAYERS = {  # name: (k, [n per shard])
+    "qkv": (5120, [6144, 1024, 1024]),
+    "o": (6144, [5120]),
+    "gate_up": (5120, [17408, 17408]),
+    "down": (17408, [5120]),
+}
+K_BITS, CODEBOOK = 3, 1  # 3 bpw, MCG
+
+
+def alg_bytes(k: int, ns: list[int], M: int, K: int) -> int:
+    """Trellis + suh per shard + svh + x in + y out (fp16), BASELINE.md C2."""
+    n = sum(ns)
+    return k * n * K // 8 + 2 * k * len(ns) + 2 * n + 2 * M * k + 2 * M * n
+
+
+def make_layer_set(torch, rng_seed: int, device):
+    g = torch.Generator(device="cpu").manual_seed(rng_seed)
+    out = {}
+    for name, (k, ns) in LAYERS.items():
+        trs, suhs, svhs = [], [], []
+        for n in ns:
+            t = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K_BITS), dtype=torch.int16, generator=g)
+            trs.append(t.to(device))
+            suhs.append((torch.randint(0, 2, (k,), generator=g) * 2 - 1).half().to(device))
+            svhs.append((torch.randint(0, 2, (n,), generator=g) * 2 - 1).half().to(device))
+        out[name] = (trs, suhs, svhs)
+    return out
+
+
+def _capture(torch, fn):
+    """HIP graph of fn() (the reference times its decode path by CUDA-graph replay, decode_microbench.py:27-41)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # first call outside capture: allocates outputs and workspace
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int):
+    """One graph holds R steps (step r: the 4 fused linears on rotating copy r).  Replays it ceil(steps / R) times
+    after ceil(warmup / R) untimed replays; returns (steps timed, ms per step, per-layer us per launch).  Per-layer
+    times come from a graph of R launches of that layer alone, timed the same way."""
+    R = len(sets)
+    names = list(LAYERS)
+    outs = {nm: torch.empty((xs[nm].shape[0], sum(LAYERS[nm][1])), dtype=torch.float16, device=xs[nm].device)
+            for nm in names}
+
+    def run(copies, layer_names):
+        for r in copies:
+            for nm in layer_names:
+                trs, suhs, svhs = sets[r][nm]
+                ops.linear(xs[nm], trs, suhs, svhs, CODEBOOK, out=outs[nm])
+
+    def timed(g, reps, warm):
+        for _ in range(warm):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    g_all = _capture(torch, lambda: run(range(R), names))
+    reps = -(-steps // R)
+    total = timed(g_all, reps, -(-warmup // R))
+    per_layer = {}
+    for nm in names:
+        g = _capture(torch, lambda nm=nm: run(range(R), [nm]))
+        lreps = max(4, reps // 2)
+        per_layer[nm] = timed(g, lreps, 2) / (lreps * R)
+    return reps * R, total / (reps * R), per_layer
+
+
+def cpu_baseline(seconds_target: float = 15.0) -> dict:
+    """The oracle (numpy restatement of trellis_core's decode + linear_forward) on one core, on a bounded sample:
+    the o_proj linear (6144 -> 5120, K = 3, MCG) at M = 1, repeated until ~seconds_target of CPU work."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import exl3_oracle as orc
+    rng = np.random.default_rng(1)
+    k, n = 6144, 5120
+    tr = rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K_BITS), dtype=np.int16)
+    suh = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+    svh = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+    reps, t_total = 0, 0.0
+    with threadpool_limits(limits=1):
+        while t_total < seconds_target and reps < 20:
+            t = time.perf_counter()
+            orc.linear_forward(x, tr, suh, svh, K_BITS, CODEBOOK)
+            t_total += time.perf_counter() - t
+            reps += 1
+    per = t_total / reps
+    b = alg_bytes(k, [n], 1, K_BITS)
+    return {"value": round(b / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle decode+linear_forward of o_proj 6144->5120 K=3 MCG M=1, {reps} reps, "
+                      f"{per * 1e3:.0f} ms each, numpy, 1 thread"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--rows", type=int, default=1)
+    ap.add_argument("--copies", type=int, default=5, help="rotating copies of the layer set (cold HBM)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--extra-rows", default="4,16", help="also report these M (comma list, '' for none)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested). "
+              "Sharding is described in DESIGN.md; run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from trellis_serve_amd import ops
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    ops.init_device(0)
+    print(f"[bench] building {args.copies} copies of the K={K_BITS} MCG layer set", file=sys.stderr, flush=True)
+    sets = [make_layer_set(torch, 1234 + r, dev) for r in range(args.copies)]
+    g = torch.Generator(device="cpu").manual_seed(7)
+
+    def xs_for(M):
+        return {nm: torch.randn((M, k), generator=g).half().to(dev) for nm, (k, _) in LAYERS.items()}
+
+    results = {}
+    for M in [args.rows] + [int(v) for v in args.extra_rows.split(",") if v and int(v) != args.rows]:
+        xs = xs_for(M)
+        steps = args.steps if M == args.rows else max(20, args.steps // 4)
+        steps, ms_step, per_layer = time_layer_set(torch, ops, sets, xs, steps, args.warmup)
+        step_bytes = sum(alg_bytes(k, ns, M, K_BITS) for k, ns in LAYERS.values())
+        results[M] = dict(ms_per_step=ms_step, gbs=step_bytes / (ms_step * 1e-3) / 1e9,
+                          per_layer=per_layer, step_bytes=step_bytes, steps=steps)
+        print(f"[bench] M={M}: {ms_step * 1e3:.1f} us/step, {results[M]['gbs']:.0f} GB/s "
+              f"per layer us {({k: round(v * 1e3, 1) for k, v in per_layer.items()})}", file=sys.stderr, flush=True)
+
+    main_r = results[args.rows]
+    # dominant kernel: the fused decode-GEMV; per-layer device time from graph replays of that layer alone
+    kern_ms = sum(main_r["per_layer"].values())
+    achieved = main_r["step_bytes"] / (kern_ms * 1e-3) / 1e9
+    line = {
+        "metric": "EXL3 decode-GEMV HBM GB/s at M=1 (27B layer set, K=3 MCG)",
+        "value": round(main_r["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": main_r["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": round(main_r["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded uniform int16 trellis codes, +-1 fp16 signs, N(0,1) fp16 activations)",
+        "config": {"workload": "27B-class dense layer set, K=3 bpw, MCG (BASELINE configs[1])",
+                   "rows": args.rows, "layers": {k: [kk, ns] for k, (kk, ns) in LAYERS.items()},
+                   "copies": args.copies, "bytes_per_step": main_r["step_bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_kernel<3, MCG> + reduce_kernel per fused linear (graph replay, HIP events)"},
+        "pct_hbm_peak": round(100 * main_r["gbs"] / HBM_PEAK_GBS, 2),
+        "us_per_layer": {k: round(v * 1e3, 2) for k, v in main_r["per_layer"].items()},
+        "other_rows": {str(M): {"GB/s": round(r["gbs"], 1), "us_per_step": round(r["ms_per_step"] * 1e3, 2)}
+                       for M, r in results.items() if M != args.rows},
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,92 @@
+/* C-ABI of the MI355X (gfx950) EXL3 hot-path library, libexl3_mi355x.so.
+ *
+ * Conventions (the reference's, cuda/csrc/exl3_marlin.cu:411-535, restated for a C boundary):
+ *   - every pointer argument is DEVICE memory unless named *_host; tensors are contiguous, row-major;
+ *   - fp16 / bf16 values are passed as raw 16-bit storage; `*_bf16` flags pick bf16 over fp16 at the boundary,
+ *     with torch's value conversions (bf16 -> fp16 round-to-nearest-even, overflow to inf; fp16 -> bf16 RNE);
+ *   - `stream` is a hipStream_t (NULL = the default stream); every call only enqueues work (no host sync,
+ *     no allocation); the caller owns every buffer, including `workspace`;
+ *   - each call returns EXL3_OK or an error code; exl3_last_error() then holds a message (thread-local).
+ *     Where the reference raised (TORCH_CHECK -> RuntimeError), this library returns EXL3_ERR_INVALID and
+ *     launches nothing.
+ *
+ * The EXL3 format (core/src/trellis_core/format/spec.py:117-160): trellis int16 [k/16, n/16, 16K], K bits per
+ * weight in {2,3,4,5,6,8}, k and n multiples of 128; suh fp16 [k], svh fp16 [n]; codebook 0 = 3INST, 1 = MCG,
+ * 2 = MUL1 (core/src/trellis_core/reference.py:24-77).
+ */
+#ifndef EXL3_MI355X_H
+#define EXL3_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_ABI_VERSION 1
+
+enum {
+  EXL3_OK = 0,
+  EXL3_ERR_INVALID = 1,     /* bad shape / argument; nothing was launched */
+  EXL3_ERR_HIP = 2,         /* a HIP runtime call failed */
+  EXL3_ERR_UNSUPPORTED = 3  /* valid request this build does not serve (e.g. not a gfx950 device) */
+};
+
+#define EXL3_MAX_SHARDS 4
+
+/* One matrix of a fused group (q/k/v, gate/up): all shards read the same input x and write adjacent column spans
+ * of y in order.  Replaces the per-shard tensors of exl3_linear_marlin_multi_out (cuda/csrc/exl3_marlin.cu:507-527)
+ * and the shard map of the Marlin template (exl3_marlin_template.h:298-302, 605-610). */
+typedef struct exl3_shard {
+  const void* trellis; /* int16 [k/16, n/16, 16K] */
+  const void* suh;     /* fp16 [k] */
+  const void* svh;     /* fp16 [n] */
+  int n;               /* output columns of this shard (multiple of 128) */
+} exl3_shard;
+
+/* ---- process / device ---------------------------------------------------------------------------------------- */
+int exl3_abi_version(void);
+const char* exl3_last_error(void);
+/* Checks that `device` is a gfx950.  Replaces init_device (cuda/csrc/exl3_marlin.cu:537). */
+int exl3_init_device(int device);
+
+/* ---- decode (subsystem 1) ------------------------------------------------------------------------------------- */
+/* W_inner fp16 [k, n] = the decoded trellis (Hadamard domain, no sign vectors), bit-identical to
+ * trellis_core.reference.reconstruct_inner (core/src/trellis_core/reference.py:102-115).  Replaces ExLlamaV3's
+ * `reconstruct` as called at cuda/src/sglang_exl3/kernels/reference.py:71-76 and xpu/csrc/exl3_ops.sycl:536. */
+int exl3_reconstruct(const void* trellis, int k, int n, int K, int codebook, void* w_out, void* stream);
+
+/* ---- Hadamard rotations (subsystem 4) ------------------------------------------------------------------------- */
+/* xh[s*rows + r, :] = fp16(Had128(fp16(x[r, :]) * suh_cat[s, :])) for shards s < shards; xh fp16 [shards*rows, k].
+ * Replaces had_in_group_marlin (cuda/csrc/exl3_marlin.cu:461-471). */
+int exl3_had_in_group(const void* x, int x_bf16, int rows, int k, const void* suh_cat, int shards, void* xh,
+                      void* stream);
+/* out[r, col0 : col0+n] = fp16(Had128(y[r, :])) * svh, stored fp16 or bf16 with row stride ld_out (elements).
+ * y fp16 [rows, n].  Replaces had_out_into_marlin (cuda/csrc/exl3_marlin.cu:475-484). */
+int exl3_had_out_into(const void* y, int rows, int n, const void* svh, void* out, int out_bf16, int ld_out, int col0,
+                      void* stream);
+
+/* ---- fused decode-GEMV / GEMM (subsystems 2, 3) --------------------------------------------------------------- */
+/* Workspace bytes exl3_linear / exl3_gemm_rotated need for `rows` rows of a group with input width k and
+ * `n_total` output columns; 0 means none.  Deterministic in its arguments. */
+size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K);
+
+/* y[rows, sum n_s] = concat_s( Had128(Had128(x * suh_s) @ W_s) * svh_s ) with fp32 accumulation; fp16 output of
+ * the GEMM, output transform as exl3_had_out_into.  x fp16|bf16 [rows, k]; y fp16|bf16 [rows, sum n_s].
+ * All shards share K and codebook.  Replaces exl3_linear_marlin_out / exl3_linear_marlin_multi_out
+ * (cuda/csrc/exl3_marlin.cu:489-527) behind torch.ops.sglang_exl3.linear (cuda/src/sglang_exl3/runtime/ops.py:133). */
+int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards, int K,
+                int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
+
+/* out fp16 [rows, n] = xh @ W_inner in the rotated basis (no Hadamards, no sign vectors); fp32 accumulation, one
+ * rounding to fp16.  Identity rows of xh read W_inner out exactly.  Replaces exl3_gemm_marlin
+ * (cuda/csrc/exl3_marlin.cu:411-423), the one-hot test entry of cuda/src/sglang_exl3/parity/marlin_parity.py:149-159. */
+int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook, void* out,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_MI355X_H */

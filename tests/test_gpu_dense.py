@@ -1,0 +1,198 @@
+"""GPU parity of the dense EXL3 path (decode, rotations, fused decode-GEMV) against the CPU oracle.
+
+Decoded weights are compared bit for bit (reconstruct and the one-hot readout through the GEMV kernel, the method of
+cuda/src/sglang_exl3/parity/marlin_parity.py:149-159 and xpu/tests/test_bitexact_xpu.py:46-102); layer outputs
+against the float64 evaluation of had(had(x*suh) @ W) * svh (parity/l1_linear.py:28-36) with the north-star gate:
+norm-relative and max-relative error <= 2e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import c_reconstruct
+from oracle import exl3_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+KS = (2, 3, 4, 5, 6, 8)
+CBS = (0, 1, 2)
+TOL = 2e-3
+
+
+def _ops():
+    from trellis_serve_amd import ops
+    return ops
+
+
+def _trellis(rng, k, n, K):
+    return rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int16)
+
+
+def _signs(rng, n):
+    return np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _errs(y, ref):
+    y = y.astype(np.float64)
+    ref = ref.astype(np.float64)
+    return (np.linalg.norm(y - ref) / np.linalg.norm(ref), np.abs(y - ref).max() / np.abs(ref).max())
+
+
+@pytest.mark.parametrize("K", KS)
+@pytest.mark.parametrize("cb", CBS)
+def test_reconstruct_is_bit_exact(coracle, K, cb):
+    rng = np.random.default_rng(1000 + 10 * K + cb)
+    tr = _trellis(rng, 128, 384, K)
+    w = _ops().reconstruct(_dev(tr), cb).cpu().numpy()
+    np.testing.assert_array_equal(w.view(np.uint16), c_reconstruct(coracle, tr, K, cb).view(np.uint16))
+
+
+@pytest.mark.parametrize("K", KS)
+@pytest.mark.parametrize("cb", CBS)
+def test_reconstruct_matches_reference_golden(golden, K, cb):
+    w = _ops().reconstruct(_dev(golden[f"recon_in_K{K}_cb{cb}"]), cb).cpu().numpy()
+    np.testing.assert_array_equal(w.view(np.uint16), golden[f"recon_out_K{K}_cb{cb}"])
+
+
+@pytest.mark.parametrize("cb", CBS)
+def test_reconstruct_covers_every_state(cb):
+    """K = 8: the state of element t is (byte[t-1] << 8) | byte[t]; 512 tiles with bytes (a, i + 128 h) put every
+    16-bit state at an odd stream position once.  Checked against the closed-form codebook."""
+    K = 8
+    tiles = np.zeros((512, 256), dtype=np.uint8)
+    for a in range(256):
+        for h in range(2):
+            tiles[2 * a + h, 0::2] = a
+            tiles[2 * a + h, 1::2] = np.arange(128) + 128 * h
+    # stream bytes MSB-first per little-endian dword -> int16 storage
+    words = tiles.reshape(512, 64, 4)
+    u32 = (words[..., 0].astype(np.uint32) << 24) | (words[..., 1].astype(np.uint32) << 16) | \
+          (words[..., 2].astype(np.uint32) << 8) | words[..., 3].astype(np.uint32)
+    tr = u32.view(np.uint16).reshape(512, 128).view(np.int16).reshape(32, 16, 128)
+    w = _ops().reconstruct(_dev(tr), cb).cpu().numpy()
+    np.testing.assert_array_equal(w.view(np.uint16), orc.reconstruct_inner(tr, K, cb).view(np.uint16))
+    perm = orc.tensor_core_perm()
+    lut = orc.codebook_lut(cb).view(np.uint16)
+    tiles_w = w.reshape(32, 16, 16, 16).transpose(0, 2, 1, 3).reshape(512, 256)[:, perm]
+    odd_states = (tiles[:, 0::2].astype(np.int64) << 8) | tiles[:, 1::2]
+    np.testing.assert_array_equal(tiles_w.view(np.uint16)[:, 1::2], lut[odd_states])
+    assert np.unique(odd_states).size == 65536
+
+
+@pytest.mark.parametrize("K", KS)
+@pytest.mark.parametrize("cb", CBS)
+def test_gemm_rotated_one_hot_readout_is_exact(coracle, K, cb):
+    rng = np.random.default_rng(2000 + 10 * K + cb)
+    k, n = 256, 256
+    tr = _trellis(rng, k, n, K)
+    xh = torch.eye(k, dtype=torch.float16, device="cuda")
+    w = _ops().gemm_rotated(xh, _dev(tr), cb).cpu().numpy()
+    np.testing.assert_array_equal(w.view(np.uint16), c_reconstruct(coracle, tr, K, cb).view(np.uint16))
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 17])
+@pytest.mark.parametrize("K,cb", [(2, 1), (3, 1), (4, 0), (5, 2), (6, 1), (8, 0)])
+def test_linear_matches_float64_oracle(coracle, M, K, cb):
+    rng = np.random.default_rng(3000 + 100 * M + 10 * K + cb)
+    k, n = 768, 640
+    tr, suh, svh = _trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)
+    x = rng.standard_normal((M, k)).astype(np.float16)
+    y = _ops().linear(_dev(x), [_dev(tr)], [_dev(suh)], [_dev(svh)], cb).cpu().numpy()
+    ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
+    nrel, mrel = _errs(y, ref)
+    assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
+
+
+def test_linear_c1_shape_4096(coracle):
+    """4096 -> 4096, K = 4, 3INST, M = 1."""
+    rng = np.random.default_rng(4096)
+    k = n = 4096
+    K, cb = 4, 0
+    tr, suh, svh = _trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)
+    x = rng.standard_normal((1, k)).astype(np.float16)
+    y = _ops().linear(_dev(x), [_dev(tr)], [_dev(suh)], [_dev(svh)], cb).cpu().numpy()
+    ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
+    nrel, mrel = _errs(y, ref)
+    assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
+
+
+def test_linear_bf16_boundary_equals_fp16_casts():
+    """run(x_bf16) == run(x_bf16.half()).bfloat16() bit for bit (cuda/src/sglang_exl3/parity/marlin_parity.py:98-111)."""
+    rng = np.random.default_rng(5)
+    k, n, K, cb = 512, 384, 3, 1
+    tr, suh, svh = _dev(_trellis(rng, k, n, K)), _dev(_signs(rng, k)), _dev(_signs(rng, n))
+    x = torch.from_numpy(rng.standard_normal((4, k)).astype(np.float32)).cuda().bfloat16()
+    y_bf = _ops().linear(x, [tr], [suh], [svh], cb)
+    y_h = _ops().linear(x.half(), [tr], [suh], [svh], cb)
+    assert y_bf.dtype == torch.bfloat16
+    assert torch.equal(y_bf, y_h.bfloat16())
+
+
+def test_linear_fused_group_matches_oracle_per_shard(coracle):
+    """q/k/v-style group: 3 shards with their own suh/svh share x and fill adjacent column spans."""
+    rng = np.random.default_rng(6)
+    k, K, cb = 512, 3, 1
+    ns = (512, 128, 256)
+    trs = [_trellis(rng, k, n, K) for n in ns]
+    suhs = [_signs(rng, k) for _ in ns]
+    svhs = [_signs(rng, n) for n in ns]
+    x = rng.standard_normal((5, k)).astype(np.float16)
+    y = _ops().linear(_dev(x), [_dev(t) for t in trs], [_dev(s) for s in suhs], [_dev(s) for s in svhs], cb)
+    y = y.cpu().numpy()
+    col = 0
+    for t, su, sv, n in zip(trs, suhs, svhs, ns):
+        ref = orc.linear_forward(x, t, su, sv, K, cb, w_inner=c_reconstruct(coracle, t, K, cb), dtype=np.float64)
+        nrel, mrel = _errs(y[:, col:col + n], ref)
+        assert nrel <= TOL and mrel <= TOL, (n, nrel, mrel)
+        col += n
+
+
+def test_linear_is_deterministic():
+    rng = np.random.default_rng(7)
+    k, n, K, cb = 2048, 1024, 3, 1
+    args = ([_dev(_trellis(rng, k, n, K))], [_dev(_signs(rng, k))], [_dev(_signs(rng, n))], cb)
+    x = _dev(rng.standard_normal((3, k)).astype(np.float16))
+    first = _ops().linear(x, *args)
+    for _ in range(20):
+        assert torch.equal(_ops().linear(x, *args), first)
+
+
+def test_had_in_group_matches_fp16_oracle():
+    rng = np.random.default_rng(8)
+    rows, k = 6, 1024
+    x = (rng.standard_normal((rows, k)) * 3).astype(np.float16)
+    suh = np.stack([_signs(rng, k), (rng.random(k) + 0.5).astype(np.float16)])
+    xh = _ops().had_in_group(_dev(x), _dev(suh)).cpu().numpy()
+    for s in range(2):
+        want = orc.had_in_fp16(x, suh[s])
+        got = xh[s * rows:(s + 1) * rows]
+        ulp = np.abs(got.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
+        assert ulp.max() <= 1 and (ulp == 0).mean() > 0.99
+
+
+def test_had_out_into_writes_its_column_span():
+    rng = np.random.default_rng(9)
+    rows, n = 3, 256
+    y = rng.standard_normal((rows, n)).astype(np.float16)
+    svh = _signs(rng, n)
+    out = torch.zeros((rows, 640), dtype=torch.float16, device="cuda")
+    _ops().had_out_into(_dev(y), _dev(svh), out, 128)
+    o = out.cpu().numpy()
+    assert not o[:, :128].any() and not o[:, 384:].any()
+    want = (orc.had_rows(y.astype(np.float32), np.float64).astype(np.float32).astype(np.float16)
+            * svh).astype(np.float16)
+    ulp = np.abs(o[:, 128:384].view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
+    assert ulp.max() <= 1
+
+
+def test_invalid_shapes_raise():
+    ops = _ops()
+    t = torch.zeros((8, 8, 48), dtype=torch.int16, device="cuda")
+    with pytest.raises(ValueError):
+        ops.linear(torch.zeros((1, 64), dtype=torch.float16, device="cuda"), [t],
+                   [torch.ones(128, dtype=torch.float16, device="cuda")],
+                   [torch.ones(128, dtype=torch.float16, device="cuda")], 1)

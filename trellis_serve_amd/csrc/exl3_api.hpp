@@ -1,0 +1,34 @@
+// Host-side helpers shared by the C-ABI translation units: status codes, the thread-local last-error string,
+// HIP error checks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/exl3_mi355x.h"
+
+namespace exl3 {
+
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define EXL3_CHECK_ARG(cond, ...)                                \
+  do {                                                           \
+    if (!(cond)) return ::exl3::set_error(EXL3_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define EXL3_CHECK_HIP(expr)                                                                      \
+  do {                                                                                            \
+    hipError_t e_ = (expr);                                                                       \
+    if (e_ != hipSuccess)                                                                         \
+      return ::exl3::set_error(EXL3_ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+  } while (0)
+
+#define EXL3_CHECK_LAUNCH() EXL3_CHECK_HIP(hipGetLastError())
+
+inline bool valid_bits(int K) { return K == 2 || K == 3 || K == 4 || K == 5 || K == 6 || K == 8; }
+inline bool valid_cb(int cb) { return cb >= 0 && cb <= 2; }
+
+}  // namespace exl3

@@ -1,0 +1,163 @@
+// Device building blocks of the EXL3 hot path on gfx950 (CDNA4, wave64).
+//
+// Format (core/src/trellis_core/reference.py:1-16): a linear's trellis is int16 [k/16, n/16, 16K]; each 16x16 tile
+// is 256*K bits, read as uint32 words w[m] = h[2m] | h[2m+1] << 16 (a little-endian dword load), bits MSB first.
+// Element t (0..255) of a tile is the codebook value of the 16-bit window that ENDS at bit (t+1)K, circular in the
+// tile (reference.py:80-99); it lands at row 8((t>>1)&1) + 2((t>>3)&3) + (t&1), column (t>>5) + 8((t>>2)&1)
+// (reference.py:30-45, the closed form of xpu/csrc/exl3_esimd.h:6-8).
+//
+// Lane geometry used by every kernel here: one wave64 owns one tile; lane l takes column c = l % 16 and the group
+// j = l / 16 of four stream-consecutive elements t0..t0+3, t0 = 32(c&7) + 4(c>>3) + 8j, which sit at rows
+// 2j, 2j+1, 2j+8, 2j+9 of column c.  Four consecutive elements need 3K+16 bits, always inside two adjacent tile
+// dwords (wrapping at the tile end for t0 = 0), so a lane loads two dwords per tile, funnels them with one
+// v_alignbit into a 32-bit chunk and pulls the four 16-bit states with v_bfe.  The group is exactly one lane's
+// slice of an MFMA 16x16x16 f16 B operand (lane l: column l%16, k-chunk l/16), so decoded values feed the matrix
+// core straight from registers; the A operand (activations) uses the same row order.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+enum Codebook : int { CB_3INST = 0, CB_MCG = 1, CB_MUL1 = 2 };
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
+
+// 1/sqrt(128) as the reference kernels write it (cuda/csrc/exl3_marlin.cu:251)
+constexpr float kHadScale = 0.088388347648f;
+
+// ---- per-lane tile geometry ----------------------------------------------------------------------------------
+struct LaneGeo {
+  int dw0, dw1;  // tile dwords holding the lane's bits (dw1 = dw0 + 1, circular)
+  int sh;        // v_alignbit shift that puts stream bit S (first window bit) at chunk bit 31
+  int pS;        // position of S inside the 64-bit pair (1..32)
+};
+
+// c: tile column 0..15, j: group 0..3
+template <int K>
+__device__ __forceinline__ LaneGeo lane_geo(int c, int j) {
+  const int t0 = 32 * (c & 7) + 4 * (c >> 3) + 8 * j;
+  const int S = (t0 + 1) * K - 16;  // first bit of element t0's window; -16 < S only wraps for t0 = 0
+  const int d0 = (S - 1) >> 5;      // floor((S-1)/32): arithmetic shift, -1 for the wrapping lane
+  LaneGeo g;
+  g.pS = S - 32 * d0;
+  g.sh = 32 - g.pS;
+  g.dw0 = (d0 + 8 * K) % (8 * K);
+  g.dw1 = (d0 + 1) % (8 * K);
+  return g;
+}
+
+// four 16-bit states of the lane's group from its two dwords (w0 = dword dw0, w1 = dword dw1)
+template <int K>
+__device__ __forceinline__ void group_states(uint32_t w0, uint32_t w1, const LaneGeo& g, uint32_t s[4]) {
+  const uint32_t ch = __builtin_amdgcn_alignbit(w0, w1, g.sh);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    if (16 - e * K >= 0)
+      s[e] = __builtin_amdgcn_ubfe(ch, 16 - e * K, 16);
+    else  // window starts beyond the first chunk (K = 6, 8 at e = 3): funnel it to the bottom
+      s[e] = __builtin_amdgcn_alignbit(w0, w1, 48 - g.pS - e * K) & 0xFFFFu;
+  }
+}
+
+// ---- codebooks (reference.py:52-73; cuda/csrc/third_party/exllamav3/codebook.cuh:28-123) --------------------
+// The 32-bit hash x = s * C (+ A) mod 2^32 with s < 2^16 runs on the fp64 FMA pipe (full rate on CDNA, unlike
+// v_mul_lo_u32): the double with bit pattern 0x43300000:s is exactly 2^52 + s, and
+// fma(2^52 + s, C, 2^52 (1 - C)) = 2^52 + s*C < 2^53 is exact, so its low dword is s*C mod 2^32.
+template <uint32_t C>
+__device__ __forceinline__ uint32_t mul_lo32(uint32_t s) {
+  const double d = __builtin_bit_cast(double, (uint64_t)s | 0x4330000000000000ull);
+  constexpr double kC = (double)C;
+  constexpr double kAdd = 4503599627370496.0 * (1.0 - kC);  // 2^52 (1 - C): 32 significant bits, exact
+  return (uint32_t)__builtin_bit_cast(uint64_t, __builtin_fma(d, kC, kAdd));
+}
+
+constexpr uint32_t kMcgMult = 0xCBAC1FEDu;
+constexpr uint32_t kMul1Mult = 0x83DCD12Du;
+constexpr uint32_t k3InstMult = 89226354u;
+constexpr uint32_t k3InstAdd = 64248484u;
+
+// fp16 pair [lo + hi of y0, lo + hi of y1], each sum rounded once (v_add_f16 == __hadd); SDWA reads the halves in
+// place and writes the second sum into the upper half, so a pair costs two VALU ops.
+__device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
+  uint32_t r;
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+      : "=&v"(r)
+      : "v"(y0), "v"(y1));
+  return r;
+}
+
+template <int CB>
+__device__ __forceinline__ uint32_t cb_hash_masked(uint32_t s) {
+  uint32_t x;
+  if constexpr (CB == CB_MCG)
+    x = mul_lo32<kMcgMult>(s);
+  else
+    x = mul_lo32<k3InstMult>(s) + k3InstAdd;
+  return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;  // one v_bitop3_b32
+}
+
+// two states -> packed fp16 [v(sa), v(sb)], bit-exact with codebook_lut
+template <int CB>
+__device__ __forceinline__ uint32_t cb_pair(uint32_t sa, uint32_t sb) {
+  if constexpr (CB == CB_MUL1) {
+    // h = fp16 bits 0x6400 + bytesum(x) = 1024 + bytesum exactly; v = fma(h, 0x1EEE, 0xC931) rounded once
+    const uint32_t ha = __builtin_amdgcn_udot4(mul_lo32<kMul1Mult>(sa), 0x01010101u, 0x6400u, false);
+    const uint32_t hb = __builtin_amdgcn_udot4(mul_lo32<kMul1Mult>(sb), 0x01010101u, 0x6400u, false);
+    const half2_t h = __builtin_bit_cast(half2_t, (hb << 16) | ha);
+    const half2_t inv = __builtin_bit_cast(half2_t, 0x1EEE1EEEu);
+    const half2_t bias = __builtin_bit_cast(half2_t, 0xC931C931u);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(h, inv, bias));
+  } else {
+    return half_sums(cb_hash_masked<CB>(sa), cb_hash_masked<CB>(sb));
+  }
+}
+
+// the lane's four decoded weights (rows 2j, 2j+1, 2j+8, 2j+9 of column c) as an MFMA operand
+template <int K, int CB>
+__device__ __forceinline__ half4_t decode_group(uint32_t w0, uint32_t w1, const LaneGeo& g) {
+  uint32_t s[4];
+  group_states<K>(w0, w1, g, s);
+  uint2_t p;
+  p.x = cb_pair<CB>(s[0], s[1]);
+  p.y = cb_pair<CB>(s[2], s[3]);
+  return __builtin_bit_cast(half4_t, p);
+}
+
+// ---- fp16 / bf16 boundary conversions (torch value conversions, RNE) -----------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40);  // NaN stays (quiet) NaN
+  u += 0x7FFFu + ((u >> 16) & 1u);                                          // round to nearest even
+  return (uint16_t)(u >> 16);
+}
+
+// ---- 128-point Hadamard on 32 lanes x 4 values (lane t holds block positions 4t..4t+3) -----------------------
+// Sylvester order: H128 = H32 (lanes) x H4 (in-lane); the in-lane part is the 4-point butterfly, the lane part five
+// xor-butterflies.  fp32 throughout, as cuda/csrc/exl3_had.cuh:20-84.
+__device__ __forceinline__ void had128_x4(float& h0, float& h1, float& h2, float& h3) {
+  const float s0 = h0 + h1, d0 = h0 - h1, s1 = h2 + h3, d1 = h2 - h3;
+  h0 = s0 + s1;
+  h1 = d0 + d1;
+  h2 = s0 - s1;
+  h3 = d0 - d1;
+  const int lane = __lane_id();
+#pragma unroll
+  for (int m = 1; m < 32; m <<= 1) {
+    const bool upper = lane & m;
+    const float o0 = __shfl_xor(h0, m, 64), o1 = __shfl_xor(h1, m, 64);
+    const float o2 = __shfl_xor(h2, m, 64), o3 = __shfl_xor(h3, m, 64);
+    h0 = upper ? o0 - h0 : h0 + o0;
+    h1 = upper ? o1 - h1 : h1 + o1;
+    h2 = upper ? o2 - h2 : h2 + o2;
+    h3 = upper ? o3 - h3 : h3 + o3;
+  }
+}
+
+}  // namespace exl3

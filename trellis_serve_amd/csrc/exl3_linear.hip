@@ -1,0 +1,478 @@
+// EXL3 dense linear on gfx950: trellis decode (reconstruct), the 128-point Hadamard rotations, and the fused
+// decode-GEMV for up to 16 rows per launch (MFMA 16x16x16 f16 fed from registers), with a deterministic split-K
+// reduce that applies the output rotation.
+//
+// Reference semantics:
+//   reconstruct        core/src/trellis_core/reference.py:102-115 (bit-exact)
+//   input rotation     cuda/csrc/exl3_had.cuh:20-84  xh = fp16(Had(fp16(x) * suh)) (fp16 product, fp32 butterfly)
+//   output rotation    cuda/csrc/exl3_had.cuh:89-117 y = fp16(Had(fp16(acc))) * svh (fp16 product)
+//   split-K reduce     cuda/csrc/exl3_marlin_template.h:2234-2262 (fixed-order fp32 sum of per-split partials)
+//   fused groups       cuda/csrc/exl3_marlin.cu:507-527 (shards share x, write adjacent column spans)
+#include <algorithm>
+
+#include "exl3_api.hpp"
+#include "exl3_device.hpp"
+
+namespace exl3 {
+
+constexpr int kGemvWaves = 8;   // one wave per tile column: a workgroup covers one 128-column block
+constexpr int kGemvRows = 16;   // rows per launch (the M of MFMA 16x16x16)
+constexpr int kGemvMaxLds = 32768;
+
+struct ShardArgs {
+  const uint32_t* trellis[EXL3_MAX_SHARDS];
+  const uint16_t* suh[EXL3_MAX_SHARDS];
+  const uint16_t* svh[EXL3_MAX_SHARDS];
+  int tn[EXL3_MAX_SHARDS];            // tile columns (n / 16)
+  int col0[EXL3_MAX_SHARDS];          // first output column
+  int blk0[EXL3_MAX_SHARDS + 1];      // first 128-column block (cumulative); blk0[count] = total blocks
+  int count;
+};
+
+__device__ __forceinline__ int find_shard(const ShardArgs& sa, int blk) {
+  int s = 0;
+#pragma unroll
+  for (int i = 1; i < EXL3_MAX_SHARDS; i++)
+    if (i < sa.count && blk >= sa.blk0[i]) s = i;
+  return s;
+}
+
+// ---- input rotation of 4 values: lane t of a 32-lane group holds block positions 4t..4t+3 --------------------
+template <bool X_BF16>
+__device__ __forceinline__ void had_in_4(const void* x_row, const uint16_t* __restrict__ suh, int kk, _Float16 h[4]) {
+  _Float16 v[4];
+  if constexpr (X_BF16) {
+    const uint2_t raw = *reinterpret_cast<const uint2_t*>(static_cast<const uint16_t*>(x_row) + kk);
+    v[0] = (_Float16)bf16_to_f32((uint16_t)(raw.x & 0xFFFF));
+    v[1] = (_Float16)bf16_to_f32((uint16_t)(raw.x >> 16));
+    v[2] = (_Float16)bf16_to_f32((uint16_t)(raw.y & 0xFFFF));
+    v[3] = (_Float16)bf16_to_f32((uint16_t)(raw.y >> 16));
+  } else {
+    const half4_t raw = *reinterpret_cast<const half4_t*>(static_cast<const uint16_t*>(x_row) + kk);
+    v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+  }
+  const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
+  float f0 = (float)(_Float16)(v[0] * su.x), f1 = (float)(_Float16)(v[1] * su.y);
+  float f2 = (float)(_Float16)(v[2] * su.z), f3 = (float)(_Float16)(v[3] * su.w);
+  had128_x4(f0, f1, f2, f3);
+  h[0] = (_Float16)(f0 * kHadScale);
+  h[1] = (_Float16)(f1 * kHadScale);
+  h[2] = (_Float16)(f2 * kHadScale);
+  h[3] = (_Float16)(f3 * kHadScale);
+}
+
+// output rotation of 4 fp16 values (lane t of a 32-lane group: block positions 4t..4t+3), then * svh
+__device__ __forceinline__ void had_out_4(_Float16 h[4], const uint16_t* __restrict__ svh4) {
+  float f0 = (float)h[0], f1 = (float)h[1], f2 = (float)h[2], f3 = (float)h[3];
+  had128_x4(f0, f1, f2, f3);
+  const half4_t sv = *reinterpret_cast<const half4_t*>(svh4);
+  h[0] = (_Float16)(f0 * kHadScale) * sv.x;
+  h[1] = (_Float16)(f1 * kHadScale) * sv.y;
+  h[2] = (_Float16)(f2 * kHadScale) * sv.z;
+  h[3] = (_Float16)(f3 * kHadScale) * sv.w;
+}
+
+template <bool BF16>
+__device__ __forceinline__ void store_4(void* row, int col, const _Float16 h[4]) {
+  if constexpr (BF16) {
+    uint2_t o;
+    o.x = (uint32_t)f32_to_bf16((float)h[0]) | ((uint32_t)f32_to_bf16((float)h[1]) << 16);
+    o.y = (uint32_t)f32_to_bf16((float)h[2]) | ((uint32_t)f32_to_bf16((float)h[3]) << 16);
+    *reinterpret_cast<uint2_t*>(static_cast<uint16_t*>(row) + col) = o;
+  } else {
+    half4_t o = {h[0], h[1], h[2], h[3]};
+    *reinterpret_cast<half4_t*>(static_cast<uint16_t*>(row) + col) = o;
+  }
+}
+
+// A-operand staging in LDS: position p of the workgroup's k-range, row m -> [m][p/16][q][e] with r = p % 16,
+// q = (r & 7) >> 1, e = (r & 1) | (r >> 3) << 1, rows mstride halves apart.  Lane (m, q) then reads its 4 activations
+// for a tile as one 8-byte word, in the row order 2q, 2q+1, 2q+8, 2q+9 the decoded B group uses, at a constant
+// 32-byte step per tile row; mstride = 16 * tile rows + 4 keeps the 16 rows of a read in distinct banks.
+__device__ __forceinline__ int a_slot(int p, int m, int mstride) {
+  const int r = p & 15;
+  return m * mstride + ((p >> 4) << 4) + (((r & 7) >> 1) << 2) + ((r & 1) | ((r >> 3) << 1));
+}
+
+// ---- reconstruct: one wave per tile -----------------------------------------------------------------------------
+template <int K, int CB>
+__global__ __launch_bounds__(256) void reconstruct_kernel(const uint32_t* __restrict__ trellis, int tk, int tn,
+                                                          uint16_t* __restrict__ w) {
+  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= tk * tn) return;
+  const int i = tile / tn, jt = tile - i * tn;
+  const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
+  const LaneGeo g = lane_geo<K>(c, j);
+  const uint32_t* tp = trellis + (size_t)tile * 8 * K;
+  const half4_t v = decode_group<K, CB>(tp[g.dw0], tp[g.dw1], g);
+  const size_t n = (size_t)tn * 16;
+  _Float16* base = reinterpret_cast<_Float16*>(w) + (size_t)16 * i * n + 16 * jt + c;
+  base[(size_t)(2 * j) * n] = v.x;
+  base[(size_t)(2 * j + 1) * n] = v.y;
+  base[(size_t)(2 * j + 8) * n] = v.z;
+  base[(size_t)(2 * j + 9) * n] = v.w;
+}
+
+// ---- standalone rotations -------------------------------------------------------------------------------------
+template <bool X_BF16>
+__global__ __launch_bounds__(256) void had_in_kernel(const void* __restrict__ x, int rows, int k,
+                                                     const uint16_t* __restrict__ suh_cat, int shards,
+                                                     uint16_t* __restrict__ xh) {
+  const int kb = k >> 7;
+  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (unit >= shards * rows * kb) return;
+  const int t = threadIdx.x & 31;
+  const int s = unit / (rows * kb), rem = unit - s * rows * kb, r = rem / kb, b = rem - r * kb;
+  const int kk = b * 128 + 4 * t;
+  _Float16 h[4];
+  had_in_4<X_BF16>(static_cast<const uint16_t*>(x) + (size_t)r * k, suh_cat + (size_t)s * k, kk, h);
+  store_4<false>(xh + ((size_t)s * rows + r) * k, kk, h);
+}
+
+template <bool OUT_BF16>
+__global__ __launch_bounds__(256) void had_out_kernel(const uint16_t* __restrict__ y, int rows, int n,
+                                                      const uint16_t* __restrict__ svh, void* __restrict__ out,
+                                                      int ld_out, int col0) {
+  const int nb = n >> 7;
+  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (unit >= rows * nb) return;
+  const int t = threadIdx.x & 31;
+  const int r = unit / nb, b = unit - r * nb;
+  const int cc = b * 128 + 4 * t;
+  const half4_t v = *reinterpret_cast<const half4_t*>(y + (size_t)r * n + cc);
+  _Float16 h[4] = {v.x, v.y, v.z, v.w};
+  had_out_4(h, svh + cc);
+  store_4<OUT_BF16>(static_cast<uint16_t*>(out) + (size_t)r * ld_out, col0 + cc, h);
+}
+
+// ---- fused decode-GEMV ------------------------------------------------------------------------------------------
+// grid (128-column blocks over all shards, k-splits); 8 waves; wave w owns tile column 8*block + w of its shard
+// and the split's k-range [kb0*128, kb1*128).  The prologue stages the split's rotated activations (IN_HAD) or the
+// given rotated activations into LDS in MFMA A order; the main loop streams the wave's tiles (two dwords per lane
+// per tile through a bounds-checked buffer descriptor, one 128-row block ahead), decodes them in registers and
+// accumulates C += A(16 x 16) * B(16 x 16) per tile on two alternating accumulators.  Each split writes its fp32
+// partial [split][m][col]; reduce_kernel sums the splits in order.
+template <int K, int CB, bool IN_HAD, bool X_BF16>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int M, int k,
+                                                                int chunk, float* __restrict__ partial, int n_total) {
+  extern __shared__ __align__(16) _Float16 xs[];
+  const int blk = blockIdx.x, split = blockIdx.y;
+  const int s = find_shard(sa, blk);
+  const int kb0 = split * chunk;
+  const int kb1 = min(k >> 7, kb0 + chunk);
+  const int nb = kb1 - kb0;
+  const int mstride = nb * 128 + 4;
+
+  // prologue: activations of the k-range, rotated (or as given), into LDS
+  {
+    const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
+    for (int u = hw; u < M * nb; u += 2 * kGemvWaves) {
+      const int m = u / nb, b = u - m * nb;
+      const int kk = (kb0 + b) * 128 + 4 * t;
+      _Float16 h[4];
+      if constexpr (IN_HAD) {
+        had_in_4<X_BF16>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
+      } else {
+        const half4_t v = *reinterpret_cast<const half4_t*>(static_cast<const uint16_t*>(x) + (size_t)m * k + kk);
+        h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
+    }
+  }
+  __syncthreads();
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
+  const int tn = sa.tn[s];
+  const int jt = (blk - sa.blk0[s]) * kGemvWaves + w;
+  const LaneGeo g = lane_geo<K>(c, j);
+  const int tile_bytes = 32 * K;
+  const int row_bytes = tn * tile_bytes;  // one tile row of the shard
+  const int nrows = k >> 4;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, nrows * row_bytes, 0x00020000);
+  const int voff0 = g.dw0 * 4, voff1 = g.dw1 * 4;
+  int soff = kb0 * 8 * row_bytes + jt * tile_bytes;  // wave-uniform
+  // A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored
+  const half4_t* ap = reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j;  // + 4 per tile row
+
+  float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  uint32_t cur0[8], cur1[8];
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    cur0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, soff + u * row_bytes, 0);
+    cur1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, soff + u * row_bytes, 0);
+  }
+  for (int b = 0; b < nb; b++) {
+    uint32_t nxt0[8], nxt1[8];
+    soff += 8 * row_bytes;
+    if (b + 1 < nb) {
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        nxt0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, soff + u * row_bytes, 0);
+        nxt1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, soff + u * row_bytes, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u += 2) {
+      const half4_t b0 = decode_group<K, CB>(cur0[u], cur1[u], g);
+      const half4_t b1 = decode_group<K, CB>(cur0[u + 1], cur1[u + 1], g);
+      const half4_t a0 = ap[(b * 8 + u) * 4];
+      const half4_t a1 = ap[(b * 8 + u + 1) * 4];
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, b1, acc1, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      cur0[u] = nxt0[u];
+      cur1[u] = nxt1[u];
+    }
+  }
+  const float4_t acc = acc0 + acc1;
+
+  // C layout: lane l holds rows 4(l/16) + r, column l % 16
+  float* dst = partial + (size_t)split * M * n_total + sa.col0[s] + jt * 16 + c;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int m = 4 * j + r;
+    if (m < M) dst[(size_t)m * n_total] = acc[r];
+  }
+}
+
+// fixed-order sum of the split partials, one rounding to fp16, then (OUT_HAD) the output rotation of each 128-column
+// block; a 32-lane group per (row, block)
+template <bool OUT_HAD, bool Y_BF16>
+__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ partial, int P, int M, int n_total,
+                                                     ShardArgs sa, void* __restrict__ y, int ldy) {
+  const int nblk = n_total >> 7;
+  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (unit >= M * nblk) return;
+  const int t = threadIdx.x & 31;
+  const int m = unit / nblk, blk = unit - m * nblk;
+  const int col = blk * 128 + 4 * t;
+  float4_t a = {0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < P; p++) a += *reinterpret_cast<const float4_t*>(partial + ((size_t)p * M + m) * n_total + col);
+  _Float16 h[4] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
+  if constexpr (OUT_HAD) {
+    const int s = find_shard(sa, blk);
+    had_out_4(h, sa.svh[s] + (col - sa.col0[s]));
+  }
+  store_4<Y_BF16>(static_cast<uint16_t*>(y) + (size_t)m * ldy, col, h);
+}
+
+// ---- host side --------------------------------------------------------------------------------------------------
+
+// k-split plan of the GEMV: enough (block, split) workgroups to fill 256 CUs several times, whole 128-row blocks
+// per split (the input rotation is blockwise), LDS for the rotated activations within kGemvMaxLds.
+struct GemvPlan {
+  int chunk, splits;
+};
+
+static GemvPlan gemv_plan(int k, int n_total, int M) {
+  const int kb = k / 128, nblk = n_total / 128;
+  const int want = (2048 + nblk - 1) / nblk;
+  int chunk = (kb + want - 1) / want;
+  chunk = std::max(1, std::min(chunk, (kGemvMaxLds / (2 * std::max(1, M)) - 4) / 128));
+  chunk = std::min(chunk, kb);
+  return {chunk, (kb + chunk - 1) / chunk};
+}
+
+#define EXL3_DISPATCH_K_CB(K_, CB_, ...)                                  \
+  [&]() -> bool {                                                         \
+    switch (K_ * 4 + CB_) {                                               \
+      EXL3_CASE_KCB(2, __VA_ARGS__) EXL3_CASE_KCB(3, __VA_ARGS__)         \
+      EXL3_CASE_KCB(4, __VA_ARGS__) EXL3_CASE_KCB(5, __VA_ARGS__)         \
+      EXL3_CASE_KCB(6, __VA_ARGS__) EXL3_CASE_KCB(8, __VA_ARGS__)         \
+      default: return false;                                              \
+    }                                                                     \
+  }()
+#define EXL3_CASE_KCB(KV, ...)                                                         \
+  case KV * 4 + 0: { constexpr int kK = KV, kCB = 0; __VA_ARGS__; return true; }      \
+  case KV * 4 + 1: { constexpr int kK = KV, kCB = 1; __VA_ARGS__; return true; }      \
+  case KV * 4 + 2: { constexpr int kK = KV, kCB = 2; __VA_ARGS__; return true; }
+
+static int build_shards(const exl3_shard* shards, int nshards, int k, int K, ShardArgs* sa, int* n_total) {
+  EXL3_CHECK_ARG(shards != nullptr && nshards >= 1 && nshards <= EXL3_MAX_SHARDS,
+                 "nshards = %d (1..%d)", nshards, EXL3_MAX_SHARDS);
+  *sa = ShardArgs{};
+  int col = 0, blk = 0;
+  for (int s = 0; s < nshards; s++) {
+    const exl3_shard& sh = shards[s];
+    EXL3_CHECK_ARG(sh.trellis && sh.suh && sh.svh, "shard %d: null tensor pointer", s);
+    EXL3_CHECK_ARG(sh.n > 0 && sh.n % 128 == 0, "shard %d: n = %d is not a positive multiple of 128", s, sh.n);
+    sa->trellis[s] = static_cast<const uint32_t*>(sh.trellis);
+    sa->suh[s] = static_cast<const uint16_t*>(sh.suh);
+    sa->svh[s] = static_cast<const uint16_t*>(sh.svh);
+    sa->tn[s] = sh.n / 16;
+    sa->col0[s] = col;
+    sa->blk0[s] = blk;
+    col += sh.n;
+    blk += sh.n / 128;
+  }
+  sa->blk0[nshards] = blk;
+  sa->count = nshards;
+  *n_total = col;
+  for (int s = 0; s < nshards; s++)
+    EXL3_CHECK_ARG((int64_t)k * shards[s].n * K / 8 <= INT32_MAX,
+                   "shard %d: trellis of %lld bytes exceeds the 2 GiB buffer range", s,
+                   (long long)((int64_t)k * shards[s].n * K / 8));
+  return EXL3_OK;
+}
+
+static int launch_gemv(const ShardArgs& sa, const void* x, bool in_had, bool x_bf16, int M, int k, int K, int cb,
+                       int n_total, float* partial, hipStream_t st, GemvPlan* out_plan) {
+  const GemvPlan pl = gemv_plan(k, n_total, M);
+  *out_plan = pl;
+  const dim3 grid(n_total / 128, pl.splits);
+  const size_t lds = (size_t)M * (pl.chunk * 128 + 4) * 2;
+  bool ok;
+  if (in_had && x_bf16)
+    ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, true><<<grid, kGemvWaves * 64, lds, st>>>(sa, x, M, k, pl.chunk, partial, n_total));
+  else if (in_had)
+    ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, false><<<grid, kGemvWaves * 64, lds, st>>>(sa, x, M, k, pl.chunk, partial, n_total));
+  else
+    ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false, false><<<grid, kGemvWaves * 64, lds, st>>>(sa, x, M, k, pl.chunk, partial, n_total));
+  if (!ok) return set_error(EXL3_ERR_INVALID, "unsupported K = %d / codebook = %d", K, cb);
+  EXL3_CHECK_LAUNCH();
+  return EXL3_OK;
+}
+
+static int launch_reduce(const ShardArgs& sa, const float* partial, int P, int M, int n_total, bool out_had,
+                         bool y_bf16, void* y, int ldy, hipStream_t st) {
+  const int units = M * (n_total / 128);
+  const dim3 grid((units + 7) / 8);
+  if (out_had && y_bf16)
+    reduce_kernel<true, true><<<grid, 256, 0, st>>>(partial, P, M, n_total, sa, y, ldy);
+  else if (out_had)
+    reduce_kernel<true, false><<<grid, 256, 0, st>>>(partial, P, M, n_total, sa, y, ldy);
+  else
+    reduce_kernel<false, false><<<grid, 256, 0, st>>>(partial, P, M, n_total, sa, y, ldy);
+  EXL3_CHECK_LAUNCH();
+  return EXL3_OK;
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_reconstruct(const void* trellis, int k, int n, int K, int codebook, void* w_out, void* stream) {
+  EXL3_CHECK_ARG(trellis && w_out, "exl3_reconstruct: null pointer");
+  EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_reconstruct: K = %d / codebook = %d", K, codebook);
+  EXL3_CHECK_ARG(k > 0 && n > 0 && k % 16 == 0 && n % 16 == 0, "exl3_reconstruct: k = %d, n = %d", k, n);
+  const int tk = k / 16, tn = n / 16;
+  const dim3 grid((unsigned)(((size_t)tk * tn + 3) / 4));
+  const bool ok = EXL3_DISPATCH_K_CB(K, codebook, reconstruct_kernel<kK, kCB><<<grid, 256, 0, as_stream(stream)>>>(
+      static_cast<const uint32_t*>(trellis), tk, tn, static_cast<uint16_t*>(w_out)));
+  if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_reconstruct: unsupported K/codebook");
+  EXL3_CHECK_LAUNCH();
+  return EXL3_OK;
+}
+
+extern "C" int exl3_had_in_group(const void* x, int x_bf16, int rows, int k, const void* suh_cat, int shards,
+                                 void* xh, void* stream) {
+  EXL3_CHECK_ARG(x && suh_cat && xh, "exl3_had_in_group: null pointer");
+  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_had_in_group: rows = %d, k = %d", rows, k);
+  EXL3_CHECK_ARG(shards >= 1 && shards <= EXL3_MAX_SHARDS, "exl3_had_in_group: shards = %d", shards);
+  if (rows == 0) return EXL3_OK;
+  const size_t units = (size_t)shards * rows * (k / 128);
+  const dim3 grid((unsigned)((units + 7) / 8));
+  if (x_bf16)
+    had_in_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(x, rows, k, static_cast<const uint16_t*>(suh_cat), shards,
+                                                             static_cast<uint16_t*>(xh));
+  else
+    had_in_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(x, rows, k, static_cast<const uint16_t*>(suh_cat), shards,
+                                                              static_cast<uint16_t*>(xh));
+  EXL3_CHECK_LAUNCH();
+  return EXL3_OK;
+}
+
+extern "C" int exl3_had_out_into(const void* y, int rows, int n, const void* svh, void* out, int out_bf16, int ld_out,
+                                 int col0, void* stream) {
+  EXL3_CHECK_ARG(y && svh && out, "exl3_had_out_into: null pointer");
+  EXL3_CHECK_ARG(rows >= 0 && n > 0 && n % 128 == 0, "exl3_had_out_into: rows = %d, n = %d", rows, n);
+  EXL3_CHECK_ARG(col0 >= 0 && col0 % 4 == 0 && ld_out >= col0 + n && ld_out % 4 == 0,
+                 "exl3_had_out_into: col0 = %d, n = %d, ld_out = %d (4-aligned, in range)", col0, n, ld_out);
+  if (rows == 0) return EXL3_OK;
+  const size_t units = (size_t)rows * (n / 128);
+  const dim3 grid((unsigned)((units + 7) / 8));
+  if (out_bf16)
+    had_out_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(static_cast<const uint16_t*>(y), rows, n,
+                                                              static_cast<const uint16_t*>(svh), out, ld_out, col0);
+  else
+    had_out_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(static_cast<const uint16_t*>(y), rows, n,
+                                                               static_cast<const uint16_t*>(svh), out, ld_out, col0);
+  EXL3_CHECK_LAUNCH();
+  return EXL3_OK;
+}
+
+extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K) {
+  (void)K;
+  if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128) return 0;
+  // launches take 16 rows at a time, then the remainder: the workspace must hold either plan's partials
+  size_t need = 0;
+  for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
+    if (M == 0) continue;
+    const GemvPlan pl = gemv_plan(k, n_total, M);
+    need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
+  }
+  return need;
+}
+
+extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards,
+                           int K, int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  EXL3_CHECK_ARG(x && y, "exl3_linear: null x / y");
+  EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_linear: K = %d / codebook = %d", K, codebook);
+  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_linear: rows = %d, k = %d", rows, k);
+  ShardArgs sa;
+  int n_total = 0;
+  if (int rc = build_shards(shards_host, nshards, k, K, &sa, &n_total)) return rc;
+  if (rows == 0) return EXL3_OK;
+  const size_t need = exl3_linear_workspace_bytes(rows, k, n_total, K);
+  EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_linear: workspace %zu bytes, need %zu", workspace_bytes,
+                 need);
+  hipStream_t st = as_stream(stream);
+  const size_t xe = 2, ye = 2;
+  for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
+    const int M = std::min(kGemvRows, rows - r0);
+    GemvPlan pl;
+    if (int rc = launch_gemv(sa, static_cast<const uint8_t*>(x) + (size_t)r0 * k * xe, true, x_bf16 != 0, M, k, K,
+                             codebook, n_total, static_cast<float*>(workspace), st, &pl))
+      return rc;
+    if (int rc = launch_reduce(sa, static_cast<const float*>(workspace), pl.splits, M, n_total, true, y_bf16 != 0,
+                               static_cast<uint8_t*>(y) + (size_t)r0 * n_total * ye, n_total, st))
+      return rc;
+  }
+  return EXL3_OK;
+}
+
+extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook,
+                                 void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  EXL3_CHECK_ARG(xh && trellis && out, "exl3_gemm_rotated: null pointer");
+  EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_gemm_rotated: K = %d / codebook = %d", K, codebook);
+  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0 && n > 0 && n % 128 == 0, "exl3_gemm_rotated: rows = %d, k = %d, n = %d",
+                 rows, k, n);
+  if (rows == 0) return EXL3_OK;
+  const size_t need = exl3_linear_workspace_bytes(rows, k, n, K);
+  EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_gemm_rotated: workspace %zu bytes, need %zu",
+                 workspace_bytes, need);
+  EXL3_CHECK_ARG((int64_t)k * n * K / 8 <= INT32_MAX, "exl3_gemm_rotated: trellis exceeds the 2 GiB buffer range");
+  ShardArgs sa{};
+  sa.trellis[0] = static_cast<const uint32_t*>(trellis);
+  sa.tn[0] = n / 16;
+  sa.blk0[1] = n / 128;
+  sa.count = 1;
+  hipStream_t st = as_stream(stream);
+  for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
+    const int M = std::min(kGemvRows, rows - r0);
+    GemvPlan pl;
+    if (int rc = launch_gemv(sa, static_cast<const uint16_t*>(xh) + (size_t)r0 * k, false, false, M, k, K, codebook, n,
+                             static_cast<float*>(workspace), st, &pl))
+      return rc;
+    if (int rc = launch_reduce(sa, static_cast<const float*>(workspace), pl.splits, M, n, false, false,
+                               static_cast<uint16_t*>(out) + (size_t)r0 * n, n, st))
+      return rc;
+  }
+  return EXL3_OK;
+}

@@ -1,0 +1,162 @@
+"""Torch-facing wrappers of the C-ABI: device tensors in, device tensors out, every launch on the current stream.
+
+These mirror the building blocks of the reference's Marlin backend (cuda/src/sglang_exl3/kernels/marlin.py:138-190)
+and ExLlamaV3's reconstruct (cuda/src/sglang_exl3/kernels/reference.py:71-76), with the same argument meaning.
+Nothing here computes on the CPU: a missing library raises ExtensionMissing.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+CODEBOOK_ID = {"3inst": 0, "mcg": 1, "mul1": 2}
+
+_workspace: dict[int, torch.Tensor] = {}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def bits_of(trellis: torch.Tensor) -> int:
+    """K from the trellis last dim (16 K int16 per tile; core/src/trellis_core/format/spec.py:58-61)."""
+    words = trellis.shape[-1]
+    if words % 16:
+        raise ValueError(f"trellis last dim {words} is not 16*K")
+    return words // 16
+
+
+def _check_trellis(t: torch.Tensor) -> tuple[int, int, int]:
+    if t.dtype != torch.int16 or t.dim() != 3 or not t.is_contiguous() or not t.is_cuda:
+        raise ValueError(f"trellis must be a contiguous CUDA int16 [k/16, n/16, 16K] tensor, got {t.dtype} "
+                         f"{tuple(t.shape)} on {t.device}")
+    return t.shape[0] * 16, t.shape[1] * 16, bits_of(t)
+
+
+def _half(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.float16 or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous CUDA fp16 tensor, got {t.dtype} on {t.device}")
+    return t
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device reusable scratch (fp32 split-K partials); grows, never shrinks (kernels/marlin.py:24-33)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    cur = _workspace.get(idx)
+    if cur is None or cur.numel() < nbytes:
+        cur = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        _workspace[idx] = cur
+    return cur
+
+
+def reserve_workspace(device: torch.device, rows: int, k: int, n_total: int, K: int) -> None:
+    workspace(device, _lib.load().exl3_linear_workspace_bytes(rows, k, n_total, K))
+
+
+def init_device(index: int) -> None:
+    _lib.check(_lib.load().exl3_init_device(int(index)), "exl3_init_device")
+
+
+def reconstruct(trellis: torch.Tensor, codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """W_inner fp16 [k, n], bit-identical to trellis_core.reference.reconstruct_inner (reference.py:102-115)."""
+    k, n, K = _check_trellis(trellis)
+    if out is None:
+        out = torch.empty((k, n), dtype=torch.float16, device=trellis.device)
+    if out.shape != (k, n) or out.dtype != torch.float16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp16 [k, n] tensor")
+    _lib.check(_lib.load().exl3_reconstruct(trellis.data_ptr(), k, n, K, int(codebook), out.data_ptr(),
+                                            _stream(trellis.device)), "reconstruct")
+    return out
+
+
+def had_in_group(x: torch.Tensor, suh_cat: torch.Tensor, xh: torch.Tensor | None = None) -> torch.Tensor:
+    """xh[s] = fp16(Had128(fp16(x) * suh_cat[s])) for all shards: x fp16|bf16 [rows, k] -> fp16 [shards*rows, k]
+    (kernels/marlin.py:138-146)."""
+    if x.dtype not in (torch.float16, torch.bfloat16) or x.dim() != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous fp16/bf16 [rows, k] tensor")
+    rows, k = x.shape
+    suh_cat = _half(suh_cat, "suh_cat")
+    shards = suh_cat.numel() // k
+    if shards * k != suh_cat.numel():
+        raise ValueError(f"suh_cat has {suh_cat.numel()} values, not a multiple of k = {k}")
+    if xh is None:
+        xh = torch.empty((shards * rows, k), dtype=torch.float16, device=x.device)
+    _lib.check(_lib.load().exl3_had_in_group(x.data_ptr(), int(x.dtype == torch.bfloat16), rows, k,
+                                             suh_cat.data_ptr(), shards, xh.data_ptr(), _stream(x.device)),
+               "had_in_group")
+    return xh
+
+
+def had_out_into(y: torch.Tensor, svh: torch.Tensor, out: torch.Tensor, col0: int) -> None:
+    """out[:, col0:col0+n] = fp16(Had128(y)) * svh in out's dtype (kernels/marlin.py:149-151)."""
+    y = _half(y, "y")
+    rows, n = y.shape
+    if out.dtype not in (torch.float16, torch.bfloat16) or out.dim() != 2 or out.stride(1) != 1:
+        raise ValueError("out must be an fp16/bf16 [rows, N] tensor with unit column stride")
+    if out.shape[0] != rows or col0 + n > out.shape[1]:
+        raise ValueError(f"out {tuple(out.shape)} cannot hold columns {col0}..{col0 + n} of {rows} rows")
+    _lib.check(_lib.load().exl3_had_out_into(y.data_ptr(), rows, n, _half(svh, "svh").data_ptr(), out.data_ptr(),
+                                             int(out.dtype == torch.bfloat16), out.stride(0), int(col0),
+                                             _stream(y.device)), "had_out_into")
+
+
+def gemm_rotated(xh: torch.Tensor, trellis: torch.Tensor, codebook: int,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """xh @ W_inner in the rotated basis, fp32 accumulation, fp16 out; identity rows read W out exactly
+    (kernels/marlin.py:153-159)."""
+    k, n, K = _check_trellis(trellis)
+    xh = _half(xh, "xh")
+    if xh.dim() != 2 or xh.shape[1] != k:
+        raise ValueError(f"xh must be [rows, {k}]")
+    rows = xh.shape[0]
+    if out is None:
+        out = torch.empty((rows, n), dtype=torch.float16, device=xh.device)
+    lib = _lib.load()
+    ws = workspace(xh.device, lib.exl3_linear_workspace_bytes(rows, k, n, K))
+    _lib.check(lib.exl3_gemm_rotated(xh.data_ptr(), rows, k, trellis.data_ptr(), n, K, int(codebook),
+                                     out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(xh.device)), "gemm_rotated")
+    return out
+
+
+def _shards(trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor]):
+    if not (1 <= len(trellis) <= _lib.MAX_SHARDS) or not (len(trellis) == len(suh) == len(svh)):
+        raise ValueError(f"1..{_lib.MAX_SHARDS} shards with one trellis, suh and svh each")
+    arr = (_lib.Exl3Shard * len(trellis))()
+    k0 = K0 = None
+    for i, (t, su, sv) in enumerate(zip(trellis, suh, svh)):
+        k, n, K = _check_trellis(t)
+        if k0 is None:
+            k0, K0 = k, K
+        if (k, K) != (k0, K0):
+            raise ValueError("all shards of a group share the input width k and the bitrate K")
+        if _half(su, "suh").numel() != k or _half(sv, "svh").numel() != n:
+            raise ValueError(f"shard {i}: suh/svh sizes {su.numel()}/{sv.numel()} != {k}/{n}")
+        arr[i] = _lib.Exl3Shard(t.data_ptr(), su.data_ptr(), sv.data_ptr(), n)
+    return arr, k0, K0
+
+
+def linear(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor],
+           codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused group: y[..., sum n_s] = concat_s(Had(Had(x * suh_s) @ W_s) * svh_s), x fp16|bf16 [..., k], y in x's
+    dtype (exl3_linear_marlin_multi_out, cuda/csrc/exl3_marlin.cu:507-527)."""
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"x must be fp16 or bf16, got {x.dtype}")
+    arr, k, K = _shards(trellis, suh, svh)
+    rows2d = x.reshape(-1, x.shape[-1]).contiguous()
+    if rows2d.shape[1] != k:
+        raise ValueError(f"x has {rows2d.shape[1]} features, the group expects {k}")
+    rows = rows2d.shape[0]
+    n_total = sum(a.n for a in arr)
+    if out is None:
+        out = torch.empty((rows, n_total), dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    ws = workspace(x.device, lib.exl3_linear_workspace_bytes(rows, k, n_total, K))
+    _lib.check(lib.exl3_linear(rows2d.data_ptr(), int(x.dtype == torch.bfloat16), rows, k, arr, len(arr), K,
+                               int(codebook), out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(),
+                               ws.numel(), _stream(x.device)), "linear")
+    return out.view(*x.shape[:-1], n_total)
