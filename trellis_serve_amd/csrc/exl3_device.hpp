@@ -64,51 +64,56 @@ __device__ __forceinline__ void group_states(uint32_t w0, uint32_t w1, const Lan
 }
 
 // ---- codebooks (reference.py:52-73; cuda/csrc/third_party/exllamav3/codebook.cuh:28-123) --------------------
-// The 32-bit hash x = s * C (+ A) mod 2^32 with s < 2^16 runs on the fp64 FMA pipe (full rate on CDNA, unlike
-// v_mul_lo_u32): the double with bit pattern 0x43300000:s is exactly 2^52 + s, and
-// fma(2^52 + s, C, 2^52 (1 - C)) = 2^52 + s*C < 2^53 is exact, so its low dword is s*C mod 2^32.
-template <uint32_t C>
-__device__ __forceinline__ uint32_t mul_lo32(uint32_t s) {
-  const double d = __builtin_bit_cast(double, (uint64_t)s | 0x4330000000000000ull);
-  constexpr double kC = (double)C;
-  constexpr double kAdd = 4503599627370496.0 * (1.0 - kC);  // 2^52 (1 - C): 32 significant bits, exact
-  return (uint32_t)__builtin_bit_cast(uint64_t, __builtin_fma(d, kC, kAdd));
-}
-
+// x = s * C (+ A) mod 2^32 with s < 2^16: one v_mul_lo_u32 (MCG, MUL1) or v_mad_u64_u32 (3INST), both full rate on
+// gfx950 (about 59 lane-ops/clk/CU measured, as fast as v_add).
 constexpr uint32_t kMcgMult = 0xCBAC1FEDu;
 constexpr uint32_t kMul1Mult = 0x83DCD12Du;
 constexpr uint32_t k3InstMult = 89226354u;
 constexpr uint32_t k3InstAdd = 64248484u;
 
-// fp16 pair [lo + hi of y0, lo + hi of y1], each sum rounded once (v_add_f16 == __hadd); SDWA reads the halves in
-// place and writes the second sum into the upper half, so a pair costs two VALU ops.
-__device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
-  uint32_t r;
-  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
-      : "=&v"(r)
-      : "v"(y0), "v"(y1));
-  return r;
-}
-
 template <int CB>
 __device__ __forceinline__ uint32_t cb_hash_masked(uint32_t s) {
   uint32_t x;
   if constexpr (CB == CB_MCG)
-    x = mul_lo32<kMcgMult>(s);
+    x = s * kMcgMult;
   else
-    x = mul_lo32<k3InstMult>(s) + k3InstAdd;
+    x = (uint32_t)((uint64_t)s * k3InstMult + k3InstAdd);
   return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;  // one v_bitop3_b32
 }
+
+// fp16 pair [lo + hi of y0, lo + hi of y1], each sum rounded once (v_add_f16 == __hadd).
+#ifndef EXL3_SDWA_HALF_SUMS
+// Two v_perm gather the low and the high halves, one v_pk_add_f16 adds them: 1.5 VALU ops per weight, all
+// visible to the compiler's hazard tracking.
+__device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
+  const uint32_t lo = __builtin_amdgcn_perm(y1, y0, 0x05040100u);  // [y0.lo, y1.lo]
+  const uint32_t hi = __builtin_amdgcn_perm(y1, y0, 0x07060302u);  // [y0.hi, y1.hi]
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, lo) + __builtin_bit_cast(half2_t, hi));
+}
+#else
+// SDWA reads the halves in place and writes the second sum into the upper half: 1 VALU op per weight.  The writes
+// are hidden from the hazard recognizer, so the block ends with the 2 wait states an MFMA needs before it may read a
+// VGPR a VALU op wrote.
+__device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
+  uint32_t r;
+  asm volatile(
+      "v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "s_nop 1"
+      : "=&v"(r)
+      : "v"(y0), "v"(y1));
+  return r;
+}
+#endif
 
 // two states -> packed fp16 [v(sa), v(sb)], bit-exact with codebook_lut
 template <int CB>
 __device__ __forceinline__ uint32_t cb_pair(uint32_t sa, uint32_t sb) {
   if constexpr (CB == CB_MUL1) {
     // h = fp16 bits 0x6400 + bytesum(x) = 1024 + bytesum exactly; v = fma(h, 0x1EEE, 0xC931) rounded once
-    const uint32_t ha = __builtin_amdgcn_udot4(mul_lo32<kMul1Mult>(sa), 0x01010101u, 0x6400u, false);
-    const uint32_t hb = __builtin_amdgcn_udot4(mul_lo32<kMul1Mult>(sb), 0x01010101u, 0x6400u, false);
-    const half2_t h = __builtin_bit_cast(half2_t, (hb << 16) | ha);
+    const uint32_t ha = __builtin_amdgcn_udot4(sa * kMul1Mult, 0x01010101u, 0x6400u, false);
+    const uint32_t hb = __builtin_amdgcn_udot4(sb * kMul1Mult, 0x01010101u, 0x6400u, false);
+    const half2_t h = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(hb, ha, 0x05040100u));
     const half2_t inv = __builtin_bit_cast(half2_t, 0x1EEE1EEEu);
     const half2_t bias = __builtin_bit_cast(half2_t, 0xC931C931u);
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(h, inv, bias));
