@@ -69,7 +69,9 @@ int exl3_had_out_into(const void* y, int rows, int n, const void* svh, void* out
 
 /* ---- fused decode-GEMV / GEMM (subsystems 2, 3) --------------------------------------------------------------- */
 /* Workspace bytes exl3_linear / exl3_gemm_rotated need for `rows` rows of a group with input width k and
- * `n_total` output columns; 0 means none.  Deterministic in its arguments. */
+ * `n_total` output columns; 0 means none.  Deterministic in its arguments.  The workspace holds per-column-block
+ * split counters and fp32 split partials: it must be zero-filled before its first use (every call leaves the
+ * counters at zero again), and calls that share a workspace must be ordered on one stream. */
 size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K);
 
 /* y[rows, sum n_s] = concat_s( Had128(Had128(x * suh_s) @ W_s) * svh_s ) with fp32 accumulation; fp16 output of

@@ -8,6 +8,8 @@
 //   output rotation    cuda/csrc/exl3_had.cuh:89-117 y = fp16(Had(fp16(acc))) * svh (fp16 product)
 //   split-K reduce     cuda/csrc/exl3_marlin_template.h:2234-2262 (fixed-order fp32 sum of per-split partials)
 //   fused groups       cuda/csrc/exl3_marlin.cu:507-527 (shards share x, write adjacent column spans)
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "exl3_api.hpp"
@@ -147,21 +149,53 @@ __global__ __launch_bounds__(256) void had_out_kernel(const uint16_t* __restrict
 
 // ---- fused decode-GEMV ------------------------------------------------------------------------------------------
 // grid (128-column blocks over all shards, k-splits); 8 waves; wave w owns tile column 8*block + w of its shard
-// and the split's k-range [kb0*128, kb1*128).  The prologue stages the split's rotated activations (IN_HAD) or the
-// given rotated activations into LDS in MFMA A order; the main loop streams the wave's tiles (two dwords per lane
-// per tile through a bounds-checked buffer descriptor, one 128-row block ahead), decodes them in registers and
-// accumulates C += A(16 x 16) * B(16 x 16) per tile on two alternating accumulators.  Each split writes its fp32
-// partial [split][m][col]; reduce_kernel sums the splits in order.
-template <int K, int CB, bool IN_HAD, bool X_BF16>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int M, int k,
-                                                                int chunk, float* __restrict__ partial, int n_total) {
+// and the split's k-range [kb0*128, kb1*128).  The wave streams its tiles through an 8-tile register ring (two
+// dwords per lane per tile, bounds-checked buffer loads): each tile is refilled with the same tile of the next
+// 128-row block as soon as it is decoded.  The first loads are issued before the prologue, which stages the split's
+// rotated activations (ROTATE) or the given ones into LDS in MFMA A order.
+// Decoded tiles feed C += A(16 x 16) * B(16 x 16) on two alternating accumulators.
+//
+// Split-K epilogue (the slot reduce of cuda/csrc/exl3_marlin_template.h:2234-2262, in one launch): every split
+// writes its fp32 partial [split][m][col]; the last split of a column block to arrive (a per-block counter in the
+// workspace) sums all partials in a fixed order, rounds once to fp16, applies the output rotation (ROTATE) and
+// stores y, then resets the counter to zero for the next call.
+constexpr int kGemvThreads = kGemvWaves * 64;
+constexpr int kCoherentDevice = 1 << 4;  // buffer cache policy sc1: device-scope coherent access
+constexpr int kWaitVmcnt0 = 0x0F70;      // s_waitcnt vmcnt(0) (expcnt, lgkmcnt unconstrained)
+
+template <int K, int CB, bool ROTATE>
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
+                                                             int M, int k, int chunk, int splits,
+                                                             float* __restrict__ partial, int* __restrict__ counters,
+                                                             void* __restrict__ y, int y_bf16, int n_total) {
   extern __shared__ __align__(16) _Float16 xs[];
+  __shared__ int last_flag;
   const int blk = blockIdx.x, split = blockIdx.y;
   const int s = find_shard(sa, blk);
   const int kb0 = split * chunk;
   const int kb1 = min(k >> 7, kb0 + chunk);
   const int nb = kb1 - kb0;
+  const int ntile = nb * 8;
   const int mstride = nb * 128 + 4;
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
+  const int tn = sa.tn[s];
+  const int jt = (blk - sa.blk0[s]) * kGemvWaves + w;
+  const LaneGeo g = lane_geo<K>(c, j);
+  const int tile_bytes = 32 * K;
+  const int row_bytes = tn * tile_bytes;  // one tile row of the shard
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, (k >> 4) * row_bytes, 0x00020000);
+  const int voff0 = g.dw0 * 4, voff1 = g.dw1 * 4;
+  const int soff0 = kb0 * 8 * row_bytes + jt * tile_bytes;  // wave-uniform: tile (kb0*8, jt)
+
+  uint32_t r0[8], r1[8];
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    r0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, soff0 + u * row_bytes, 0);
+    r1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, soff0 + u * row_bytes, 0);
+  }
 
   // prologue: activations of the k-range, rotated (or as given), into LDS
   {
@@ -170,8 +204,11 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(ShardArgs sa, con
       const int m = u / nb, b = u - m * nb;
       const int kk = (kb0 + b) * 128 + 4 * t;
       _Float16 h[4];
-      if constexpr (IN_HAD) {
-        had_in_4<X_BF16>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
+      if constexpr (ROTATE) {
+        if (x_bf16)
+          had_in_4<true>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
+        else
+          had_in_4<false>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
       } else {
         const half4_t v = *reinterpret_cast<const half4_t*>(static_cast<const uint16_t*>(x) + (size_t)m * k + kk);
         h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
@@ -182,101 +219,119 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(ShardArgs sa, con
   }
   __syncthreads();
 
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
-  const int tn = sa.tn[s];
-  const int jt = (blk - sa.blk0[s]) * kGemvWaves + w;
-  const LaneGeo g = lane_geo<K>(c, j);
-  const int tile_bytes = 32 * K;
-  const int row_bytes = tn * tile_bytes;  // one tile row of the shard
-  const int nrows = k >> 4;
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, nrows * row_bytes, 0x00020000);
-  const int voff0 = g.dw0 * 4, voff1 = g.dw1 * 4;
-  int soff = kb0 * 8 * row_bytes + jt * tile_bytes;  // wave-uniform
-  // A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored
+  // Main loop, branch-free so the in-order vmcnt waits stay exact: tile u of block b is decoded, its registers are
+  // refilled with tile u of block b+1 (the last block re-reads itself: cache hits, never used), and it feeds one
+  // MFMA.  A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored.
   const half4_t* ap = reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j;  // + 4 per tile row
-
   float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  uint32_t cur0[8], cur1[8];
-#pragma unroll
-  for (int u = 0; u < 8; u++) {
-    cur0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, soff + u * row_bytes, 0);
-    cur1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, soff + u * row_bytes, 0);
-  }
   for (int b = 0; b < nb; b++) {
-    uint32_t nxt0[8], nxt1[8];
-    soff += 8 * row_bytes;
-    if (b + 1 < nb) {
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        nxt0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, soff + u * row_bytes, 0);
-        nxt1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, soff + u * row_bytes, 0);
-      }
-    }
+    const int nsoff = soff0 + min(b + 1, nb - 1) * 8 * row_bytes;
 #pragma unroll
     for (int u = 0; u < 8; u += 2) {
-      const half4_t b0 = decode_group<K, CB>(cur0[u], cur1[u], g);
-      const half4_t b1 = decode_group<K, CB>(cur0[u + 1], cur1[u + 1], g);
-      const half4_t a0 = ap[(b * 8 + u) * 4];
-      const half4_t a1 = ap[(b * 8 + u + 1) * 4];
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, b1, acc1, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      cur0[u] = nxt0[u];
-      cur1[u] = nxt1[u];
+      const half4_t b0 = decode_group<K, CB>(r0[u], r1[u], g);
+      const half4_t b1 = decode_group<K, CB>(r0[u + 1], r1[u + 1], g);
+      r0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, nsoff + u * row_bytes, 0);
+      r1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, nsoff + u * row_bytes, 0);
+      r0[u + 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, nsoff + (u + 1) * row_bytes, 0);
+      r1[u + 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, nsoff + (u + 1) * row_bytes, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], b0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u + 1) * 4], b1, acc1, 0, 0, 0);
     }
   }
   const float4_t acc = acc0 + acc1;
 
-  // C layout: lane l holds rows 4(l/16) + r, column l % 16
-  float* dst = partial + (size_t)split * M * n_total + sa.col0[s] + jt * 16 + c;
+  // this split's partial; C layout: lane l holds rows 4(l/16) + r, column l % 16.  Partials cross XCDs (each XCD
+  // has its own L2), so they are written and read with device-scope coherence (sc1: write-through, no stale L2
+  // hits) instead of a device-scope fence, which would write back this XCD's whole L2.
+  const int col_blk = blk * 128;  // first column of the block in y / partial
+  const __amdgpu_buffer_rsrc_t prsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)partial, (short)0, splits * M * n_total * 4, 0x00020000);
+  float* pdst = partial + (size_t)split * M * n_total + col_blk + w * 16 + c;
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int m = 4 * j + r;
-    if (m < M) dst[(size_t)m * n_total] = acc[r];
+    if (m < M) __hip_atomic_store(pdst + (size_t)m * n_total, acc[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this thread's partial stores are at the coherence point
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(&counters[blk], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = prev == splits - 1;
+  }
+  __syncthreads();
+  if (!last_flag) return;
 
-// fixed-order sum of the split partials, one rounding to fp16, then (OUT_HAD) the output rotation of each 128-column
-// block; a 32-lane group per (row, block)
-template <bool OUT_HAD, bool Y_BF16>
-__global__ __launch_bounds__(256) void reduce_kernel(const float* __restrict__ partial, int P, int M, int n_total,
-                                                     ShardArgs sa, void* __restrict__ y, int ldy) {
-  const int nblk = n_total >> 7;
-  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (unit >= M * nblk) return;
-  const int t = threadIdx.x & 31;
-  const int m = unit / nblk, blk = unit - m * nblk;
-  const int col = blk * 128 + 4 * t;
-  float4_t a = {0.f, 0.f, 0.f, 0.f};
-  for (int p = 0; p < P; p++) a += *reinterpret_cast<const float4_t*>(partial + ((size_t)p * M + m) * n_total + col);
-  _Float16 h[4] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
-  if constexpr (OUT_HAD) {
-    const int s = find_shard(sa, blk);
-    had_out_4(h, sa.svh[s] + (col - sa.col0[s]));
+  // last split of this column block: units (row m, 4-column group q); p-groups G share the splits p = g, g + G, ...
+  // and are combined in a fixed order
+  float4_t* red = reinterpret_cast<float4_t*>(xs);  // reuse the activation LDS (>= 512 * 16 B reserved)
+  const int units = M * 32;
+  const int G = max(1, kGemvThreads / units);
+  const int tid = threadIdx.x;
+  if (tid < units * G) {
+    const int unit = tid % units, gq = tid / units;
+    const int m = unit >> 5, q = unit & 31;
+    const int base = (m * n_total + col_blk + 4 * q) * 4;
+    const int pstride = M * n_total * 4;
+    float4_t a = {0.f, 0.f, 0.f, 0.f};
+    int p = gq;
+    for (; p + 3 * G < splits; p += 4 * G) {
+      const float4_t v0 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + p * pstride, 0, kCoherentDevice));
+      const float4_t v1 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + (p + G) * pstride, 0, kCoherentDevice));
+      const float4_t v2 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + (p + 2 * G) * pstride, 0, kCoherentDevice));
+      const float4_t v3 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + (p + 3 * G) * pstride, 0, kCoherentDevice));
+      a += v0; a += v1; a += v2; a += v3;
+    }
+    for (; p < splits; p += G)
+      a += __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + p * pstride, 0, kCoherentDevice));
+    red[gq * units + unit] = a;
   }
-  store_4<Y_BF16>(static_cast<uint16_t*>(y) + (size_t)m * ldy, col, h);
+  __syncthreads();
+  if (tid < units) {
+    float4_t a = red[tid];
+    for (int gq = 1; gq < G; gq++) a += red[gq * units + tid];
+    const int m = tid >> 5, q = tid & 31;
+    _Float16 h[4] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
+    const int col = col_blk + 4 * q;
+    if constexpr (ROTATE) had_out_4(h, sa.svh[s] + (col - sa.col0[s]));
+    uint16_t* yrow = static_cast<uint16_t*>(y) + (size_t)m * n_total;
+    if (y_bf16)
+      store_4<true>(yrow, col, h);
+    else
+      store_4<false>(yrow, col, h);
+  }
+  if (tid == 0) __hip_atomic_store(&counters[blk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side --------------------------------------------------------------------------------------------------
 
 // k-split plan of the GEMV: enough (block, split) workgroups to fill 256 CUs several times, whole 128-row blocks
-// per split (the input rotation is blockwise), LDS for the rotated activations within kGemvMaxLds.
+// per split (the input rotation is blockwise), LDS for the rotated activations within kGemvMaxLds and at least the
+// 16 * 128 fp32 the epilogue reduces in.
 struct GemvPlan {
   int chunk, splits;
+  size_t lds;
 };
+
+static int gemv_target_wgs() {
+  static const int v = [] {
+    const char* e = getenv("EXL3_GEMV_TARGET_WGS");
+    return e ? std::max(1, atoi(e)) : 2048;
+  }();
+  return v;
+}
 
 static GemvPlan gemv_plan(int k, int n_total, int M) {
   const int kb = k / 128, nblk = n_total / 128;
-  const int want = (2048 + nblk - 1) / nblk;
+  const int want = (gemv_target_wgs() + nblk - 1) / nblk;
   int chunk = (kb + want - 1) / want;
   chunk = std::max(1, std::min(chunk, (kGemvMaxLds / (2 * std::max(1, M)) - 4) / 128));
   chunk = std::min(chunk, kb);
-  return {chunk, (kb + chunk - 1) / chunk};
+  const size_t lds = std::max<size_t>((size_t)M * (chunk * 128 + 4) * 2, (size_t)kGemvThreads * 16);
+  return {chunk, (kb + chunk - 1) / chunk, lds};
 }
+
+// workspace layout: [counters: one int per 128-column block, zero between calls][pad to 256 B][fp32 partials]
+static size_t counters_bytes(int n_total) { return ((size_t)(n_total / 128) * sizeof(int) + 255) & ~(size_t)255; }
 
 #define EXL3_DISPATCH_K_CB(K_, CB_, ...)                                  \
   [&]() -> bool {                                                         \
@@ -301,6 +356,8 @@ static int build_shards(const exl3_shard* shards, int nshards, int k, int K, Sha
     const exl3_shard& sh = shards[s];
     EXL3_CHECK_ARG(sh.trellis && sh.suh && sh.svh, "shard %d: null tensor pointer", s);
     EXL3_CHECK_ARG(sh.n > 0 && sh.n % 128 == 0, "shard %d: n = %d is not a positive multiple of 128", s, sh.n);
+    EXL3_CHECK_ARG((int64_t)k * sh.n * K / 8 <= INT32_MAX, "shard %d: trellis of %lld bytes exceeds the 2 GiB buffer range",
+                   s, (long long)((int64_t)k * sh.n * K / 8));
     sa->trellis[s] = static_cast<const uint32_t*>(sh.trellis);
     sa->suh[s] = static_cast<const uint16_t*>(sh.suh);
     sa->svh[s] = static_cast<const uint16_t*>(sh.svh);
@@ -313,42 +370,30 @@ static int build_shards(const exl3_shard* shards, int nshards, int k, int K, Sha
   sa->blk0[nshards] = blk;
   sa->count = nshards;
   *n_total = col;
-  for (int s = 0; s < nshards; s++)
-    EXL3_CHECK_ARG((int64_t)k * shards[s].n * K / 8 <= INT32_MAX,
-                   "shard %d: trellis of %lld bytes exceeds the 2 GiB buffer range", s,
-                   (long long)((int64_t)k * shards[s].n * K / 8));
   return EXL3_OK;
 }
 
-static int launch_gemv(const ShardArgs& sa, const void* x, bool in_had, bool x_bf16, int M, int k, int K, int cb,
-                       int n_total, float* partial, hipStream_t st, GemvPlan* out_plan) {
-  const GemvPlan pl = gemv_plan(k, n_total, M);
-  *out_plan = pl;
-  const dim3 grid(n_total / 128, pl.splits);
-  const size_t lds = (size_t)M * (pl.chunk * 128 + 4) * 2;
-  bool ok;
-  if (in_had && x_bf16)
-    ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, true><<<grid, kGemvWaves * 64, lds, st>>>(sa, x, M, k, pl.chunk, partial, n_total));
-  else if (in_had)
-    ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, false><<<grid, kGemvWaves * 64, lds, st>>>(sa, x, M, k, pl.chunk, partial, n_total));
-  else
-    ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false, false><<<grid, kGemvWaves * 64, lds, st>>>(sa, x, M, k, pl.chunk, partial, n_total));
-  if (!ok) return set_error(EXL3_ERR_INVALID, "unsupported K = %d / codebook = %d", K, cb);
-  EXL3_CHECK_LAUNCH();
-  return EXL3_OK;
-}
-
-static int launch_reduce(const ShardArgs& sa, const float* partial, int P, int M, int n_total, bool out_had,
-                         bool y_bf16, void* y, int ldy, hipStream_t st) {
-  const int units = M * (n_total / 128);
-  const dim3 grid((units + 7) / 8);
-  if (out_had && y_bf16)
-    reduce_kernel<true, true><<<grid, 256, 0, st>>>(partial, P, M, n_total, sa, y, ldy);
-  else if (out_had)
-    reduce_kernel<true, false><<<grid, 256, 0, st>>>(partial, P, M, n_total, sa, y, ldy);
-  else
-    reduce_kernel<false, false><<<grid, 256, 0, st>>>(partial, P, M, n_total, sa, y, ldy);
-  EXL3_CHECK_LAUNCH();
+// one launch per 16 rows: decode-GEMV + in-launch split reduce (+ rotations when `rotate`)
+static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_bf16, int rows, int k, int K, int cb,
+                       int n_total, void* workspace, void* y, bool y_bf16, hipStream_t st) {
+  int* counters = static_cast<int*>(workspace);
+  float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total));
+  for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
+    const int M = std::min(kGemvRows, rows - r0);
+    const GemvPlan pl = gemv_plan(k, n_total, M);
+    const dim3 grid(n_total / 128, pl.splits);
+    const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * k * 2;
+    void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
+    bool ok;
+    if (rotate)
+      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true><<<grid, kGemvThreads, pl.lds, st>>>(
+          sa, xr, (int)x_bf16, M, k, pl.chunk, pl.splits, partial, counters, yr, (int)y_bf16, n_total));
+    else
+      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false><<<grid, kGemvThreads, pl.lds, st>>>(
+          sa, xr, (int)x_bf16, M, k, pl.chunk, pl.splits, partial, counters, yr, (int)y_bf16, n_total));
+    if (!ok) return set_error(EXL3_ERR_INVALID, "unsupported K = %d / codebook = %d", K, cb);
+    EXL3_CHECK_LAUNCH();
+  }
   return EXL3_OK;
 }
 
@@ -416,7 +461,7 @@ extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int 
     const GemvPlan pl = gemv_plan(k, n_total, M);
     need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
   }
-  return need;
+  return counters_bytes(n_total) + need;
 }
 
 extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards,
@@ -432,47 +477,25 @@ extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl
   const size_t need = exl3_linear_workspace_bytes(rows, k, n_total, K);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_linear: workspace %zu bytes, need %zu", workspace_bytes,
                  need);
-  hipStream_t st = as_stream(stream);
-  const size_t xe = 2, ye = 2;
-  for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
-    const int M = std::min(kGemvRows, rows - r0);
-    GemvPlan pl;
-    if (int rc = launch_gemv(sa, static_cast<const uint8_t*>(x) + (size_t)r0 * k * xe, true, x_bf16 != 0, M, k, K,
-                             codebook, n_total, static_cast<float*>(workspace), st, &pl))
-      return rc;
-    if (int rc = launch_reduce(sa, static_cast<const float*>(workspace), pl.splits, M, n_total, true, y_bf16 != 0,
-                               static_cast<uint8_t*>(y) + (size_t)r0 * n_total * ye, n_total, st))
-      return rc;
-  }
-  return EXL3_OK;
+  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, workspace, y, y_bf16 != 0,
+                     as_stream(stream));
 }
 
 extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook,
                                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
   EXL3_CHECK_ARG(xh && trellis && out, "exl3_gemm_rotated: null pointer");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_gemm_rotated: K = %d / codebook = %d", K, codebook);
-  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0 && n > 0 && n % 128 == 0, "exl3_gemm_rotated: rows = %d, k = %d, n = %d",
-                 rows, k, n);
+  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0 && n > 0 && n % 128 == 0,
+                 "exl3_gemm_rotated: rows = %d, k = %d, n = %d", rows, k, n);
+  EXL3_CHECK_ARG((int64_t)k * n * K / 8 <= INT32_MAX, "exl3_gemm_rotated: trellis exceeds the 2 GiB buffer range");
   if (rows == 0) return EXL3_OK;
   const size_t need = exl3_linear_workspace_bytes(rows, k, n, K);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_gemm_rotated: workspace %zu bytes, need %zu",
                  workspace_bytes, need);
-  EXL3_CHECK_ARG((int64_t)k * n * K / 8 <= INT32_MAX, "exl3_gemm_rotated: trellis exceeds the 2 GiB buffer range");
   ShardArgs sa{};
   sa.trellis[0] = static_cast<const uint32_t*>(trellis);
   sa.tn[0] = n / 16;
   sa.blk0[1] = n / 128;
   sa.count = 1;
-  hipStream_t st = as_stream(stream);
-  for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
-    const int M = std::min(kGemvRows, rows - r0);
-    GemvPlan pl;
-    if (int rc = launch_gemv(sa, static_cast<const uint16_t*>(xh) + (size_t)r0 * k, false, false, M, k, K, codebook, n,
-                             static_cast<float*>(workspace), st, &pl))
-      return rc;
-    if (int rc = launch_reduce(sa, static_cast<const float*>(workspace), pl.splits, M, n, false, false,
-                               static_cast<uint16_t*>(out) + (size_t)r0 * n, n, st))
-      return rc;
-  }
-  return EXL3_OK;
+  return launch_gemv(sa, xh, false, false, rows, k, K, codebook, n, workspace, out, false, as_stream(stream));
 }

@@ -45,11 +45,12 @@ def _half(t: torch.Tensor, name: str) -> torch.Tensor:
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device reusable scratch (fp32 split-K partials); grows, never shrinks (kernels/marlin.py:24-33)."""
+    """Per-device reusable scratch (split counters + fp32 split-K partials); grows, never shrinks
+    (kernels/marlin.py:24-33).  Zero-filled once at allocation: the kernels leave the counters at zero."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     cur = _workspace.get(idx)
     if cur is None or cur.numel() < nbytes:
-        cur = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        cur = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
         _workspace[idx] = cur
     return cur
 
