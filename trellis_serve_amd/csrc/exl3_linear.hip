@@ -19,7 +19,7 @@ namespace exl3 {
 
 constexpr int kGemvWaves = 8;   // one wave per tile column: a workgroup covers one 128-column block
 constexpr int kGemvRows = 16;   // rows per launch (the M of MFMA 16x16x16)
-constexpr int kGemvMaxLds = 32768;
+constexpr int kGemvMaxLds = 65536;  // dynamic LDS limit of a workgroup without opt-in
 
 struct ShardArgs {
   const uint32_t* trellis[EXL3_MAX_SHARDS];
@@ -149,11 +149,17 @@ __global__ __launch_bounds__(256) void had_out_kernel(const uint16_t* __restrict
 
 // ---- fused decode-GEMV ------------------------------------------------------------------------------------------
 // grid (128-column blocks over all shards, k-splits); 8 waves; wave w owns tile column 8*block + w of its shard
-// and the split's k-range [kb0*128, kb1*128).  The wave streams its tiles through an 8-tile register ring (two
-// dwords per lane per tile, bounds-checked buffer loads): each tile is refilled with the same tile of the next
-// 128-row block as soon as it is decoded.  The first loads are issued before the prologue, which stages the split's
+// and NT tile rows (NB = NT/8 blocks of 128 rows) starting at block kb0 = split * NB.
+//
+// Streaming: a block's 8 tiles of the wave's column (8 x 32K bytes, 96 B apart at K = 3) arrive with one or two
+// wave-wide 16-byte-per-lane gathers (the texture addresser spends the same cycles on a 4-byte and a 16-byte lane,
+// so wide lanes cut its work about 8x against per-tile dword gathers), are written to a wave-private LDS stage, and
+// each lane then reads the two dwords of its group per tile from LDS.  Two blocks are in flight.  The code is
+// straight-line (NT is a template parameter): no loop-carried load registers, exact in-order vmcnt waits.  A split
+// shorter than NT rows (the last one) clamps its loads to its last block and sees zero activations past its end.
+//
+// Every decoded tile feeds one MFMA 16x16x16 f16 on two alternating accumulators.  The prologue stages the split's
 // rotated activations (ROTATE) or the given ones into LDS in MFMA A order.
-// Decoded tiles feed C += A(16 x 16) * B(16 x 16) on two alternating accumulators.
 //
 // Split-K epilogue (the slot reduce of cuda/csrc/exl3_marlin_template.h:2234-2262, in one launch): every split
 // writes its fp32 partial [split][m][col]; the last split of a column block to arrive (a per-block counter in the
@@ -163,20 +169,32 @@ constexpr int kGemvThreads = kGemvWaves * 64;
 constexpr int kCoherentDevice = 1 << 4;  // buffer cache policy sc1: device-scope coherent access
 constexpr int kWaitVmcnt0 = 0x0F70;      // s_waitcnt vmcnt(0) (expcnt, lgkmcnt unconstrained)
 
-template <int K, int CB, bool ROTATE>
+// LDS bytes of the GEMV: staged activations (M rows of NT*16 + 4 halves), then per wave two block stages of 256*K
+// bytes; at least 16 * 128 fp32 for the epilogue reduce
+__host__ __device__ constexpr int gemv_a_bytes(int M, int NT) { return ((M * (NT * 16 + 4) * 2) + 15) & ~15; }
+__host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K) {
+  return gemv_a_bytes(M, NT) + kGemvWaves * 2 * 256 * K > kGemvThreads * 16
+             ? gemv_a_bytes(M, NT) + kGemvWaves * 2 * 256 * K
+             : kGemvThreads * 16;
+}
+
+template <int K, int CB, bool ROTATE, int NT>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
-                                                             int M, int k, int chunk, int splits,
-                                                             float* __restrict__ partial, int* __restrict__ counters,
-                                                             void* __restrict__ y, int y_bf16, int n_total) {
-  extern __shared__ __align__(16) _Float16 xs[];
+                                                             int M, int k, int splits, float* __restrict__ partial,
+                                                             int* __restrict__ counters, void* __restrict__ y,
+                                                             int y_bf16, int n_total) {
+  constexpr int NB = NT / 8;               // 128-row blocks per split
+  constexpr int CHUNKS = 16 * K;           // 16-byte chunks in the 8 tiles of one block column
+  constexpr int LPB = (CHUNKS + 63) / 64;  // wave-wide gathers per block
+  constexpr int STAGE = 256 * K;           // bytes of one block stage
+  extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
+  _Float16* xs = reinterpret_cast<_Float16*>(lds);
   const int blk = blockIdx.x, split = blockIdx.y;
   const int s = find_shard(sa, blk);
-  const int kb0 = split * chunk;
-  const int kb1 = min(k >> 7, kb0 + chunk);
-  const int nb = kb1 - kb0;
-  const int ntile = nb * 8;
-  const int mstride = nb * 128 + 4;
+  const int kb0 = split * NB;
+  const int nb = min(k >> 7, kb0 + NB) - kb0;  // blocks of this split holding data (1..NB)
+  const int mstride = NT * 16 + 4;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
@@ -187,31 +205,49 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   const int row_bytes = tn * tile_bytes;  // one tile row of the shard
   const __amdgpu_buffer_rsrc_t rsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, (k >> 4) * row_bytes, 0x00020000);
-  const int voff0 = g.dw0 * 4, voff1 = g.dw1 * 4;
   const int soff0 = kb0 * 8 * row_bytes + jt * tile_bytes;  // wave-uniform: tile (kb0*8, jt)
 
-  uint32_t r0[8], r1[8];
+  // gather lane mapping: chunk L = i*64 + lane -> tile row L / (2K) of the block, 16-byte piece L % (2K); it lands at
+  // stage byte 16 L, so each tile sits contiguously at stage byte 32K * row
+  int goff[LPB];
+  bool glive[LPB];
 #pragma unroll
-  for (int u = 0; u < 8; u++) {
-    r0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, soff0 + u * row_bytes, 0);
-    r1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, soff0 + u * row_bytes, 0);
+  for (int i = 0; i < LPB; i++) {
+    const int L = i * 64 + l;
+    glive[i] = L < CHUNKS;
+    goff[i] = (L / (2 * K)) * row_bytes + (L % (2 * K)) * 16;
   }
+  uint8_t* stage_base = lds + gemv_a_bytes(M, NT) + w * 2 * STAGE;
 
-  // prologue: activations of the k-range, rotated (or as given), into LDS
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 buf[NB][LPB];
+  auto issue = [&](int b) {
+    const int so = soff0 + min(b, nb - 1) * 8 * row_bytes;
+#pragma unroll
+    for (int i = 0; i < LPB; i++)
+      buf[b][i] = glive[i] ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, goff[i], so, 0))
+                           : u32x4{0, 0, 0, 0};
+  };
+  issue(0);
+  if constexpr (NB > 1) issue(1);
+
+  // prologue: activations of the split, rotated (or as given), into LDS; blocks past the split's end are zero
   {
     const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
-    for (int u = hw; u < M * nb; u += 2 * kGemvWaves) {
-      const int m = u / nb, b = u - m * nb;
+    for (int u = hw; u < M * NB; u += 2 * kGemvWaves) {
+      const int m = u / NB, b = u - m * NB;
       const int kk = (kb0 + b) * 128 + 4 * t;
-      _Float16 h[4];
-      if constexpr (ROTATE) {
-        if (x_bf16)
-          had_in_4<true>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
-        else
-          had_in_4<false>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
-      } else {
-        const half4_t v = *reinterpret_cast<const half4_t*>(static_cast<const uint16_t*>(x) + (size_t)m * k + kk);
-        h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
+      _Float16 h[4] = {0, 0, 0, 0};
+      if (b < nb) {
+        if constexpr (ROTATE) {
+          if (x_bf16)
+            had_in_4<true>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
+          else
+            had_in_4<false>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
+        } else {
+          const half4_t v = *reinterpret_cast<const half4_t*>(static_cast<const uint16_t*>(x) + (size_t)m * k + kk);
+          h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
@@ -219,23 +255,24 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   }
   __syncthreads();
 
-  // Main loop, branch-free so the in-order vmcnt waits stay exact: tile u of block b is decoded, its registers are
-  // refilled with tile u of block b+1 (the last block re-reads itself: cache hits, never used), and it feeds one
-  // MFMA.  A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored.
+  // A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored
   const half4_t* ap = reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j;  // + 4 per tile row
   float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  for (int b = 0; b < nb; b++) {
-    const int nsoff = soff0 + min(b + 1, nb - 1) * 8 * row_bytes;
 #pragma unroll
-    for (int u = 0; u < 8; u += 2) {
-      const half4_t b0 = decode_group<K, CB>(r0[u], r1[u], g);
-      const half4_t b1 = decode_group<K, CB>(r0[u + 1], r1[u + 1], g);
-      r0[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, nsoff + u * row_bytes, 0);
-      r1[u] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, nsoff + u * row_bytes, 0);
-      r0[u + 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff0, nsoff + (u + 1) * row_bytes, 0);
-      r1[u + 1] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, voff1, nsoff + (u + 1) * row_bytes, 0);
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], b0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u + 1) * 4], b1, acc1, 0, 0, 0);
+  for (int b = 0; b < NB; b++) {
+    uint8_t* st = stage_base + (b & 1) * STAGE;
+#pragma unroll
+    for (int i = 0; i < LPB; i++)
+      if (glive[i]) *reinterpret_cast<u32x4*>(st + 16 * (i * 64 + l)) = buf[b][i];
+    if (b + 2 < NB) issue(b + 2);
+    const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const half4_t bv = decode_group<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
+      if (u & 1)
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc1, 0, 0, 0);
+      else
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc0, 0, 0, 0);
     }
   }
   const float4_t acc = acc0 + acc1;
@@ -263,7 +300,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
   // last split of this column block: units (row m, 4-column group q); p-groups G share the splits p = g, g + G, ...
   // and are combined in a fixed order
-  float4_t* red = reinterpret_cast<float4_t*>(xs);  // reuse the activation LDS (>= 512 * 16 B reserved)
+  float4_t* red = reinterpret_cast<float4_t*>(lds);  // reuse the LDS (>= 512 * 16 B reserved)
   const int units = M * 32;
   const int G = max(1, kGemvThreads / units);
   const int tid = threadIdx.x;
@@ -304,30 +341,33 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
 // ---- host side --------------------------------------------------------------------------------------------------
 
-// k-split plan of the GEMV: enough (block, split) workgroups to fill 256 CUs several times, whole 128-row blocks
-// per split (the input rotation is blockwise), LDS for the rotated activations within kGemvMaxLds and at least the
-// 16 * 128 fp32 the epilogue reduces in.
+// k-split plan of the GEMV: NT tile rows per split (a template instance: 16, 32 or 64), the largest that still gives
+// enough (block, split) workgroups to fill the 256 CUs, LDS for the staged activations (and >= 16 * 128 fp32 for
+// the epilogue reduce).
 struct GemvPlan {
-  int chunk, splits;
+  int nt, splits;
   size_t lds;
 };
 
 static int gemv_target_wgs() {
   static const int v = [] {
     const char* e = getenv("EXL3_GEMV_TARGET_WGS");
-    return e ? std::max(1, atoi(e)) : 2048;
+    return e ? std::max(1, atoi(e)) : 1536;
   }();
   return v;
 }
 
-static GemvPlan gemv_plan(int k, int n_total, int M) {
+static GemvPlan gemv_plan(int k, int n_total, int M, int K) {
   const int kb = k / 128, nblk = n_total / 128;
-  const int want = (gemv_target_wgs() + nblk - 1) / nblk;
-  int chunk = (kb + want - 1) / want;
-  chunk = std::max(1, std::min(chunk, (kGemvMaxLds / (2 * std::max(1, M)) - 4) / 128));
-  chunk = std::min(chunk, kb);
-  const size_t lds = std::max<size_t>((size_t)M * (chunk * 128 + 4) * 2, (size_t)kGemvThreads * 16);
-  return {chunk, (kb + chunk - 1) / chunk, lds};
+  int nt = 16;
+  for (int cand : {64, 32}) {
+    const int splits = (kb + cand / 8 - 1) / (cand / 8);
+    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs() && gemv_lds_bytes(M, cand, K) <= kGemvMaxLds) {
+      nt = cand;
+      break;
+    }
+  }
+  return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(M, nt, K)};
 }
 
 // workspace layout: [counters: one int per 128-column block, zero between calls][pad to 256 B][fp32 partials]
@@ -380,17 +420,24 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
   float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total));
   for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
     const int M = std::min(kGemvRows, rows - r0);
-    const GemvPlan pl = gemv_plan(k, n_total, M);
+    const GemvPlan pl = gemv_plan(k, n_total, M, K);
     const dim3 grid(n_total / 128, pl.splits);
     const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * k * 2;
     void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
-    bool ok;
-    if (rotate)
-      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true><<<grid, kGemvThreads, pl.lds, st>>>(
-          sa, xr, (int)x_bf16, M, k, pl.chunk, pl.splits, partial, counters, yr, (int)y_bf16, n_total));
-    else
-      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false><<<grid, kGemvThreads, pl.lds, st>>>(
-          sa, xr, (int)x_bf16, M, k, pl.chunk, pl.splits, partial, counters, yr, (int)y_bf16, n_total));
+    bool ok = false;
+#define EXL3_GEMV_LAUNCH(NTV)                                                                                        \
+  if (pl.nt == NTV) {                                                                                                \
+    if (rotate)                                                                                                      \
+      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, NTV><<<grid, kGemvThreads, pl.lds, st>>>(           \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+    else                                                                                                             \
+      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false, NTV><<<grid, kGemvThreads, pl.lds, st>>>(          \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+  }
+    EXL3_GEMV_LAUNCH(16)
+    EXL3_GEMV_LAUNCH(32)
+    EXL3_GEMV_LAUNCH(64)
+#undef EXL3_GEMV_LAUNCH
     if (!ok) return set_error(EXL3_ERR_INVALID, "unsupported K = %d / codebook = %d", K, cb);
     EXL3_CHECK_LAUNCH();
   }
@@ -458,7 +505,7 @@ extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int 
   size_t need = 0;
   for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
     if (M == 0) continue;
-    const GemvPlan pl = gemv_plan(k, n_total, M);
+    const GemvPlan pl = gemv_plan(k, n_total, M, K);
     need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
   }
   return counters_bytes(n_total) + need;
