@@ -82,27 +82,26 @@ __device__ __forceinline__ uint32_t cb_hash_masked(uint32_t s) {
 }
 
 // fp16 pair [lo + hi of y0, lo + hi of y1], each sum rounded once (v_add_f16 == __hadd).
-#ifndef EXL3_SDWA_HALF_SUMS
-// Two v_perm gather the low and the high halves, one v_pk_add_f16 adds them: 1.5 VALU ops per weight, all
-// visible to the compiler's hazard tracking.
+#ifndef EXL3_PERM_HALF_SUMS
+// SDWA reads the halves in place and writes the second sum into the upper half: one VALU op per weight.  The
+// compiler cannot see the VGPR writes inside the asm, so the block ends with the wait states an MFMA needs before
+// reading a VGPR a VALU op wrote (without them the next MFMA has read a stale B operand).
+__device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
+  uint32_t r;
+  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+      "s_nop 2"
+      : "=&v"(r)
+      : "v"(y0), "v"(y1));
+  return r;
+}
+#else
+// Two v_perm gather the low and the high halves, one v_pk_add_f16 adds them: 1.5 VALU ops per weight, all visible
+// to the compiler's hazard tracking.
 __device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
   const uint32_t lo = __builtin_amdgcn_perm(y1, y0, 0x05040100u);  // [y0.lo, y1.lo]
   const uint32_t hi = __builtin_amdgcn_perm(y1, y0, 0x07060302u);  // [y0.hi, y1.hi]
   return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, lo) + __builtin_bit_cast(half2_t, hi));
-}
-#else
-// SDWA reads the halves in place and writes the second sum into the upper half: 1 VALU op per weight.  The writes
-// are hidden from the hazard recognizer, so the block ends with the 2 wait states an MFMA needs before it may read a
-// VGPR a VALU op wrote.
-__device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
-  uint32_t r;
-  asm volatile(
-      "v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-      "s_nop 1"
-      : "=&v"(r)
-      : "v"(y0), "v"(y1));
-  return r;
 }
 #endif
 

@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void had_out_kernel(const uint16_t* __restrict
 // Streaming: a block's 8 tiles of the wave's column (8 x 32K bytes, 96 B apart at K = 3) arrive with one or two
 // wave-wide 16-byte-per-lane gathers (the texture addresser spends the same cycles on a 4-byte and a 16-byte lane,
 // so wide lanes cut its work about 8x against per-tile dword gathers), are written to a wave-private LDS stage, and
-// each lane then reads the two dwords of its group per tile from LDS.  Two blocks are in flight.  The code is
+// each lane then reads the two dwords of its group per tile from LDS.  Three blocks are in flight.  The code is
 // straight-line (NT is a template parameter): no loop-carried load registers, exact in-order vmcnt waits.  A split
 // shorter than NT rows (the last one) clamps its loads to its last block and sees zero activations past its end.
 //
@@ -230,6 +230,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   };
   issue(0);
   if constexpr (NB > 1) issue(1);
+  if constexpr (NB > 2) issue(2);
 
   // prologue: activations of the split, rotated (or as given), into LDS; blocks past the split's end are zero
   {
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 #pragma unroll
     for (int i = 0; i < LPB; i++)
       if (glive[i]) *reinterpret_cast<u32x4*>(st + 16 * (i * 64 + l)) = buf[b][i];
-    if (b + 2 < NB) issue(b + 2);
+    if (b + 3 < NB) issue(b + 3);
     const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
 #pragma unroll
     for (int u = 0; u < 8; u++) {
