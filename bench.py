@@ -16,9 +16,13 @@ decode-GEMM rate when that path is present.
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -134,6 +138,73 @@ def cpu_baseline(seconds_target: float = 15.0) -> dict:
                       f"{per * 1e3:.0f} ms each, numpy, 1 thread"}
 
 
+DOMINANT = "gate_up"  # the largest fused linear: its gemv_kernel instance is the dominant kernel of a step
+
+
+def _under_profiler() -> bool:
+    return any(k.startswith(("ROCPROF_", "ROCPROFILER_")) for k in os.environ)
+
+
+def probe(kind: str, launches: int) -> int:
+    """Short GPU programs for counter passes: `gate_up` launches the dominant GEMV kernel `launches` times on one copy
+    of the layer; `copy` runs a plain 512 MiB device copy (the calibration of FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+
+    from trellis_serve_amd import ops
+    dev = torch.device("cuda", 0)
+    if kind == "copy":
+        src = torch.empty(128 << 20, dtype=torch.float32, device=dev).uniform_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+    else:
+        k, ns = LAYERS[kind]
+        s = make_layer_set(torch, 99, dev)[kind]
+        x = torch.randn((1, k), dtype=torch.float16, device=dev)
+        out = ops.linear(x, *s, CODEBOOK)
+        for _ in range(launches):
+            ops.linear(x, *s, CODEBOOK, out=out)
+    torch.cuda.synchronize()
+    return 0
+
+
+def _pmc_pass(counter: str, kind: str, name_filter: str) -> float | None:
+    """Mean per-dispatch value of `counter` over the dispatches whose kernel name contains `name_filter` (the
+    largest-valued dispatch for the copy probe), from `rocprofv3 --pmc` on `bench.py --probe kind`."""
+    with tempfile.TemporaryDirectory() as d:
+        cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d,
+               "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--probe", kind]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if r.returncode != 0 or not files:
+            print(f"[bench] counter pass {counter}/{kind} failed (rc {r.returncode}): {r.stderr[-400:]}",
+                  file=sys.stderr, flush=True)
+            return None
+        vals = [float(row["Counter_Value"]) for row in csv.DictReader(open(files[0]))
+                if row["Counter_Name"] == counter and name_filter in row["Kernel_Name"]]
+    if not vals:
+        return None
+    return max(vals) if kind == "copy" else sum(vals) / len(vals)
+
+
+def measure_traffic() -> dict | None:
+    """HBM bytes per launch of the dominant GEMV kernel from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled
+    by what the same counter reads for a plain copy of 512 MiB."""
+    copy_bytes = 512 << 20
+    got = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        kern = _pmc_pass(counter, DOMINANT, "gemv_kernel")
+        cal = _pmc_pass(counter, "copy", "")
+        if kern is None or not cal:
+            return None
+        got[counter] = (kern, cal, copy_bytes / (cal * 1024.0))
+    fetch = got["FETCH_SIZE"][0] * 1024.0 * got["FETCH_SIZE"][2]
+    write = got["WRITE_SIZE"][0] * 1024.0 * got["WRITE_SIZE"][2]
+    return {"bytes": fetch + write, "fetch_bytes": fetch, "write_bytes": write,
+            "fetch_kib_raw": got["FETCH_SIZE"][0], "write_kib_raw": got["WRITE_SIZE"][0],
+            "fetch_scale": got["FETCH_SIZE"][2], "write_scale": got["WRITE_SIZE"][2]}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,11 +214,21 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=5, help="rotating copies of the layer set (cold HBM)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--extra-rows", default="4,16", help="also report these M (comma list, '' for none)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--probe", choices=["gate_up", "copy"], help=argparse.SUPPRESS)
+    ap.add_argument("--probe-launches", type=int, default=20, help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.probe:
+        return probe(args.probe, args.probe_launches)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested). "
               "Sharding is described in DESIGN.md; run with --gpus 1.", file=sys.stderr)
         return 2
+
+    traffic = None
+    if not args.no_traffic and not _under_profiler():
+        print("[bench] counter passes (FETCH_SIZE, WRITE_SIZE) on the dominant kernel", file=sys.stderr, flush=True)
+        traffic = measure_traffic()
 
     import torch
 
@@ -174,9 +255,13 @@ def main() -> int:
               f"per layer us {({k: round(v * 1e3, 1) for k, v in per_layer.items()})}", file=sys.stderr, flush=True)
 
     main_r = results[args.rows]
-    # dominant kernel: the fused decode-GEMV; per-layer device time from graph replays of that layer alone
-    kern_ms = sum(main_r["per_layer"].values())
-    achieved = main_r["step_bytes"] / (kern_ms * 1e-3) / 1e9
+    # dominant kernel: the gate_up fused linear (one gemv_kernel launch); its per-launch time comes from HIP events
+    # around graph replays of that layer alone
+    kd, nd = LAYERS[DOMINANT]
+    dom_bytes = alg_bytes(kd, nd, args.rows, K_BITS)
+    dom_ms = main_r["per_layer"][DOMINANT]
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    all_ms = sum(main_r["per_layer"].values())
     line = {
         "metric": "EXL3 decode-GEMV HBM GB/s at M=1 (27B layer set, K=3 MCG)",
         "value": round(main_r["gbs"], 2),
@@ -194,13 +279,20 @@ def main() -> int:
                    "rows": args.rows, "layers": {k: [kk, ns] for k, (kk, ns) in LAYERS.items()},
                    "copies": args.copies, "bytes_per_step": main_r["step_bytes"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<3, MCG> + reduce_kernel per fused linear (graph replay, HIP events)"},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else round(traffic["bytes"]),
+                     "kernel": f"gemv_kernel<{K_BITS}, MCG, rotate, NT> of the {DOMINANT} linear "
+                               f"({kd}->{'+'.join(map(str, nd))}), {dom_bytes} algorithmic bytes per launch",
+                     "us_per_launch": round(dom_ms * 1e3, 2)},
         "pct_hbm_peak": round(100 * main_r["gbs"] / HBM_PEAK_GBS, 2),
         "us_per_layer": {k: round(v * 1e3, 2) for k, v in main_r["per_layer"].items()},
+        "gemv_kernels_gbs": round(main_r["step_bytes"] / (all_ms * 1e-3) / 1e9, 2),
         "other_rows": {str(M): {"GB/s": round(r["gbs"], 1), "us_per_step": round(r["ms_per_step"] * 1e3, 2)}
                        for M, r in results.items() if M != args.rows},
     }
+    if traffic is not None:
+        line["roofline"]["traffic_detail"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                              for k, v in traffic.items()}
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline()
