@@ -1,0 +1,85 @@
+"""GPU parity of the fused prefill decode-GEMM (exl3_linear_prefill) against the float64 oracle, and against the
+decode-GEMV path on the same inputs.  Gate: norm-relative and max-relative error <= 2e-3."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import c_reconstruct
+from oracle import exl3_oracle as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _ops():
+    from trellis_serve_amd import ops
+    return ops
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _case(rng, k, n, K):
+    tr = rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int16)
+    suh = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16)
+    svh = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16)
+    return tr, suh, svh
+
+
+def _errs(y, ref):
+    y = y.astype(np.float64)
+    return np.linalg.norm(y - ref) / np.linalg.norm(ref), np.abs(y - ref).max() / np.abs(ref).max()
+
+
+@pytest.mark.parametrize("M", [1, 37, 256, 300])
+@pytest.mark.parametrize("K,cb", [(2, 0), (3, 1), (4, 2), (5, 1), (6, 0), (8, 2)])
+def test_prefill_matches_float64_oracle(coracle, M, K, cb):
+    rng = np.random.default_rng(7000 + 10 * K + cb + M)
+    k, n = 512, 384
+    tr, suh, svh = _case(rng, k, n, K)
+    x = (rng.standard_normal((M, k)) * 0.5).astype(np.float16)
+    y = _ops().linear_prefill(_dev(x), [_dev(tr)], [_dev(suh)], [_dev(svh)], cb).cpu().numpy()
+    ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
+    nrel, mrel = _errs(y, ref)
+    assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
+
+
+def test_prefill_fused_group_and_bf16(coracle):
+    rng = np.random.default_rng(11)
+    k, K, cb, M = 640, 3, 1, 300
+    ns = (512, 128, 256)
+    cases = [_case(rng, k, n, K) for n in ns]
+    x = (rng.standard_normal((M, k)) * 0.5).astype(np.float16)
+    args = ([_dev(c[0]) for c in cases], [_dev(c[1]) for c in cases], [_dev(c[2]) for c in cases], cb)
+    y = _ops().linear_prefill(_dev(x), *args).cpu().numpy()
+    col = 0
+    for (tr, suh, svh), n in zip(cases, ns):
+        ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
+        nrel, mrel = _errs(y[:, col:col + n], ref)
+        assert nrel <= TOL and mrel <= TOL, (n, nrel, mrel)
+        col += n
+    xb = _dev(x).bfloat16()
+    yb = _ops().linear_prefill(xb, *args)
+    assert yb.dtype == torch.bfloat16
+    assert torch.equal(yb, _ops().linear_prefill(xb.half(), *args).bfloat16())
+
+
+def test_prefill_agrees_with_gemv_path():
+    rng = np.random.default_rng(12)
+    k, n, K, cb, M = 1024, 1024, 4, 1, 64
+    tr, suh, svh = (_dev(a) for a in _case(rng, k, n, K))
+    x = torch.randn((M, k), device="cuda").half()
+    a = _ops().linear_prefill(x, [tr], [suh], [svh], cb).float()
+    b = _ops().linear(x, [tr], [suh], [svh], cb).float()
+    assert ((a - b).norm() / b.norm()).item() < 1e-3
+
+
+def test_prefill_is_deterministic():
+    rng = np.random.default_rng(13)
+    k, n, K, cb, M = 1024, 512, 3, 1, 513
+    args = ([_dev(a) for a in _case(rng, k, n, K)[:1]], [_dev(_case(rng, k, n, K)[1])], [_dev(_case(rng, k, n, K)[2])], cb)
+    x = torch.randn((M, k), device="cuda").half()
+    first = _ops().linear_prefill(x, *args)
+    for _ in range(5):
+        assert torch.equal(_ops().linear_prefill(x, *args), first)

@@ -29,6 +29,10 @@ typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 // 1/sqrt(128) as the reference kernels write it (cuda/csrc/exl3_marlin.cu:251)
 constexpr float kHadScale = 0.088388347648f;
 
+// s_waitcnt immediate for "vmcnt <= n" with expcnt and lgkmcnt unconstrained (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8)
+__host__ __device__ constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
 // ---- per-lane tile geometry ----------------------------------------------------------------------------------
 struct LaneGeo {
   int dw0, dw1;  // tile dwords holding the lane's bits (dw1 = dw0 + 1, circular)

@@ -13,6 +13,7 @@ from . import _lib
 CODEBOOK_ID = {"3inst": 0, "mcg": 1, "mul1": 2}
 
 _workspace: dict[int, torch.Tensor] = {}
+_prefill_ws: dict[int, torch.Tensor] = {}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -160,4 +161,32 @@ def linear(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor]
     _lib.check(lib.exl3_linear(rows2d.data_ptr(), int(x.dtype == torch.bfloat16), rows, k, arr, len(arr), K,
                                int(codebook), out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(),
                                ws.numel(), _stream(x.device)), "linear")
+    return out.view(*x.shape[:-1], n_total)
+
+
+def linear_prefill(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor],
+                   codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Many-row form of `linear`: input rotations into a per-device workspace, then the fused decode-GEMM (weights
+    decoded into LDS, fp16 MFMA).  Same result contract as `linear` (the reference's prefill branch,
+    cuda/src/sglang_exl3/runtime/ops.py:87-95)."""
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"x must be fp16 or bf16, got {x.dtype}")
+    arr, k, K = _shards(trellis, suh, svh)
+    rows2d = x.reshape(-1, x.shape[-1]).contiguous()
+    if rows2d.shape[1] != k:
+        raise ValueError(f"x has {rows2d.shape[1]} features, the group expects {k}")
+    rows = rows2d.shape[0]
+    n_total = sum(a.n for a in arr)
+    if out is None:
+        out = torch.empty((rows, n_total), dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    need = lib.exl3_prefill_workspace_bytes(rows, k, len(arr))
+    idx = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    ws = _prefill_ws.get(idx)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+        _prefill_ws[idx] = ws
+    _lib.check(lib.exl3_linear_prefill(rows2d.data_ptr(), int(x.dtype == torch.bfloat16), rows, k, arr, len(arr), K,
+                                       int(codebook), out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(),
+                                       ws.numel(), _stream(x.device)), "linear_prefill")
     return out.view(*x.shape[:-1], n_total)
