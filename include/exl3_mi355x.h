@@ -97,6 +97,33 @@ size_t exl3_prefill_workspace_bytes(int rows, int k, int nshards);
 int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards, int K,
                         int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- MoE grouped experts (subsystem 5a) --------------------------------------------------------------------------- */
+/* Stacked expert weights of one MoE layer (SiLU-gated, no routed scaling: the contract of the reference's
+ * Exl3MoEMethod, cuda/src/sglang_exl3/sglang_glue/moe.py:109-119).  All experts share K and the codebook. */
+typedef struct exl3_moe_weights {
+  const void* gate_trellis; /* int16 [E][H/16][I/16][16K] */
+  const void* up_trellis;   /* int16 [E][H/16][I/16][16K] */
+  const void* down_trellis; /* int16 [E][I/16][H/16][16K] */
+  const void* gate_suh;     /* fp16 [E][H] */
+  const void* gate_svh;     /* fp16 [E][I] */
+  const void* up_suh;       /* fp16 [E][H] */
+  const void* up_svh;       /* fp16 [E][I] */
+  const void* down_suh;     /* fp16 [E][I] */
+  const void* down_svh;     /* fp16 [E][H] */
+} exl3_moe_weights;
+
+/* Workspace bytes of exl3_moe_forward (routing lists, fp16 g|u and down rows, split counters, fp32 partials).  Must
+ * be zero-filled before its first use (the split counters return to zero after every call). */
+size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K);
+/* y[t] = sum_j w[t, j] * down_e(fp16(silu(gate_e(x[t])) * up_e(x[t]))), e = topk_ids[t, j]; every linear is an EXL3
+ * linear with its own suh / svh; fp32 combine in slot order; ids outside [0, E) are skipped.  x fp16|bf16 [T, H],
+ * topk_ids int32 [T, top_k], topk_weights fp32 [T, top_k], y fp16|bf16 [T, H].  Replaces the five launches of
+ * cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294 (moe_had_in, moe_gemm, moe_glu_had_in, moe_gemm,
+ * moe_combine; cuda/csrc/exl3_marlin_moe.cu:376-499) and the align step (exl3_marlin_moe.cu:532-594). */
+int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids, const void* topk_weights,
+                     int top_k, int num_experts, int inter, const exl3_moe_weights* weights_host, int K, int codebook,
+                     void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

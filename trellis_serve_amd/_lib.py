@@ -35,6 +35,11 @@ class Exl3Shard(ctypes.Structure):
                 ("n", ctypes.c_int)]
 
 
+class Exl3MoeWeights(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in ("gate_trellis", "up_trellis", "down_trellis", "gate_suh",
+                                                      "gate_svh", "up_suh", "up_svh", "down_suh", "down_svh")]
+
+
 _P, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 _SIGNATURES: dict[str, tuple] = {
     "exl3_abi_version": (_I, []),
@@ -48,6 +53,9 @@ _SIGNATURES: dict[str, tuple] = {
     "exl3_gemm_rotated": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _P, _SZ, _P]),
     "exl3_prefill_workspace_bytes": (_SZ, [_I, _I, _I]),
     "exl3_linear_prefill": (_I, [_P, _I, _I, _I, ctypes.POINTER(Exl3Shard), _I, _I, _I, _P, _I, _P, _SZ, _P]),
+    "exl3_moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "exl3_moe_forward": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, ctypes.POINTER(Exl3MoeWeights), _I, _I, _P, _I,
+                              _P, _SZ, _P]),
 }
 
 _lib = None

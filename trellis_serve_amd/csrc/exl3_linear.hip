@@ -14,6 +14,7 @@
 
 #include "exl3_api.hpp"
 #include "exl3_device.hpp"
+#include "exl3_stream.hpp"
 
 namespace exl3 {
 
@@ -85,15 +86,6 @@ __device__ __forceinline__ void store_4(void* row, int col, const _Float16 h[4])
     half4_t o = {h[0], h[1], h[2], h[3]};
     *reinterpret_cast<half4_t*>(static_cast<uint16_t*>(row) + col) = o;
   }
-}
-
-// A-operand staging in LDS: position p of the workgroup's k-range, row m -> [m][p/16][q][e] with r = p % 16,
-// q = (r & 7) >> 1, e = (r & 1) | (r >> 3) << 1, rows mstride halves apart.  Lane (m, q) then reads its 4 activations
-// for a tile as one 8-byte word, in the row order 2q, 2q+1, 2q+8, 2q+9 the decoded B group uses, at a constant
-// 32-byte step per tile row; mstride = 16 * tile rows + 4 keeps the 16 rows of a read in distinct banks.
-__device__ __forceinline__ int a_slot(int p, int m, int mstride) {
-  const int r = p & 15;
-  return m * mstride + ((p >> 4) << 4) + (((r & 7) >> 1) << 2) + ((r & 1) | ((r >> 3) << 1));
 }
 
 // ---- reconstruct: one wave per tile -----------------------------------------------------------------------------
@@ -183,10 +175,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
                                                              int M, int k, int splits, float* __restrict__ partial,
                                                              int* __restrict__ counters, void* __restrict__ y,
                                                              int y_bf16, int n_total) {
-  constexpr int NB = NT / 8;               // 128-row blocks per split
-  constexpr int CHUNKS = 16 * K;           // 16-byte chunks in the 8 tiles of one block column
-  constexpr int LPB = (CHUNKS + 63) / 64;  // wave-wide gathers per block
-  constexpr int STAGE = 256 * K;           // bytes of one block stage
+  typedef TileStream<K, CB, NT> Stream;
+  constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
@@ -199,38 +189,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
   const int tn = sa.tn[s];
-  const int jt = (blk - sa.blk0[s]) * kGemvWaves + w;
-  const LaneGeo g = lane_geo<K>(c, j);
-  const int tile_bytes = 32 * K;
-  const int row_bytes = tn * tile_bytes;  // one tile row of the shard
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, (k >> 4) * row_bytes, 0x00020000);
-  const int soff0 = kb0 * 8 * row_bytes + jt * tile_bytes;  // wave-uniform: tile (kb0*8, jt)
-
-  // gather lane mapping: chunk L = i*64 + lane -> tile row L / (2K) of the block, 16-byte piece L % (2K); it lands at
-  // stage byte 16 L, so each tile sits contiguously at stage byte 32K * row
-  int goff[LPB];
-  bool glive[LPB];
-#pragma unroll
-  for (int i = 0; i < LPB; i++) {
-    const int L = i * 64 + l;
-    glive[i] = L < CHUNKS;
-    goff[i] = (L / (2 * K)) * row_bytes + (L % (2 * K)) * 16;
-  }
-  uint8_t* stage_base = lds + gemv_a_bytes(M, NT) + w * 2 * STAGE;
-
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 buf[NB][LPB];
-  auto issue = [&](int b) {
-    const int so = soff0 + min(b, nb - 1) * 8 * row_bytes;
-#pragma unroll
-    for (int i = 0; i < LPB; i++)
-      buf[b][i] = glive[i] ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, goff[i], so, 0))
-                           : u32x4{0, 0, 0, 0};
-  };
-  issue(0);
-  if constexpr (NB > 1) issue(1);
-  if constexpr (NB > 2) issue(2);
+  Stream stream;
+  stream.init(sa.trellis[s], (k >> 4) * tn * 32 * K, tn, (blk - sa.blk0[s]) * kGemvWaves + w, kb0, nb,
+              lds + gemv_a_bytes(M, NT) + w * Stream::LDS_BYTES, l);
+  stream.start();
 
   // prologue: activations of the split, rotated (or as given), into LDS; blocks past the split's end are zero
   {
@@ -257,26 +219,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   __syncthreads();
 
   // A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored
-  const half4_t* ap = reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j;  // + 4 per tile row
-  float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int b = 0; b < NB; b++) {
-    uint8_t* st = stage_base + (b & 1) * STAGE;
-#pragma unroll
-    for (int i = 0; i < LPB; i++)
-      if (glive[i]) *reinterpret_cast<u32x4*>(st + 16 * (i * 64 + l)) = buf[b][i];
-    if (b + 3 < NB) issue(b + 3);
-    const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const half4_t bv = decode_group<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
-      if (u & 1)
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc1, 0, 0, 0);
-      else
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc0, 0, 0, 0);
-    }
-  }
-  const float4_t acc = acc0 + acc1;
+  const float4_t acc = stream.run(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j);
+
 
   // this split's partial; C layout: lane l holds rows 4(l/16) + r, column l % 16.  Partials cross XCDs (each XCD
   // has its own L2), so they are written and read with device-scope coherence (sc1: write-through, no stale L2

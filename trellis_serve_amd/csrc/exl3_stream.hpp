@@ -1,0 +1,109 @@
+// Per-wave weight streaming for the decode-GEMV family (dense linear, MoE experts).
+//
+// One wave owns one tile column (16 output columns) and NT tile rows (NB = NT/8 blocks of 128 rows) of a trellis.
+// A block's 8 tiles of that column (8 x 32K bytes, one tile row apart) arrive with one or two wave-wide
+// 16-byte-per-lane gathers -- the texture addresser spends the same cycles on a 4-byte and a 16-byte lane, so wide
+// lanes cut its work about 8x against per-tile dword gathers -- are written to a wave-private LDS stage, and each
+// lane reads the two dwords of its group per tile from LDS (lane geometry of exl3_device.hpp).  Three blocks are in
+// flight in registers.  Everything is straight-line code (NT is a template parameter): no loop-carried load
+// registers, exact in-order vmcnt waits.  A stream shorter than NT rows (a split's tail) clamps its loads to its
+// last block; the caller gives it zero activations past its end.
+//
+// Every decoded tile feeds one MFMA 16x16x16 f16 whose A operand (the activations, staged in LDS by the caller in
+// the same row order as the decoded group: rows 2q, 2q+1, 2q+8, 2q+9 for k-chunk q) is read at a 32-byte step per
+// tile row.
+#pragma once
+#include "exl3_device.hpp"
+
+namespace exl3 {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int K, int CB, int NT>
+struct TileStream {
+  static constexpr int NB = NT / 8;               // 128-row blocks
+  static constexpr int CHUNKS = 16 * K;           // 16-byte chunks in the 8 tiles of one block column
+  static constexpr int LPB = (CHUNKS + 63) / 64;  // wave-wide gathers per block
+  static constexpr int STAGE = 256 * K;           // bytes of one block stage
+  static constexpr int LDS_BYTES = 2 * STAGE;     // per wave
+
+  __amdgpu_buffer_rsrc_t rsrc;
+  int soff0, row_bytes, nb, lane;
+  int goff[LPB];
+  bool glive[LPB];
+  u32x4_t buf[NB][LPB];
+  uint8_t* stage;
+  LaneGeo g;
+
+  // trellis: base of the matrix (int16 [k/16, n/16, 16K]); total_bytes: its size; tile_col: the wave's tile column;
+  // kb0: first 128-row block; nblocks: blocks holding data (1..NB); stage_lds: the wave's LDS_BYTES
+  __device__ __forceinline__ void init(const void* trellis, int total_bytes, int tn, int tile_col, int kb0,
+                                       int nblocks, uint8_t* stage_lds, int l) {
+    const int tile_bytes = 32 * K;
+    row_bytes = tn * tile_bytes;
+    rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)trellis, (short)0, total_bytes, 0x00020000);
+    soff0 = kb0 * 8 * row_bytes + tile_col * tile_bytes;
+    nb = nblocks;
+    lane = l;
+    stage = stage_lds;
+    g = lane_geo<K>(l & 15, l >> 4);
+    // chunk L = i*64 + lane -> tile row L / (2K) of the block, 16-byte piece L % (2K); it lands at stage byte 16 L,
+    // so each tile sits contiguously at stage byte 32K * row
+#pragma unroll
+    for (int i = 0; i < LPB; i++) {
+      const int L = i * 64 + l;
+      glive[i] = L < CHUNKS;
+      goff[i] = (L / (2 * K)) * row_bytes + (L % (2 * K)) * 16;
+    }
+  }
+
+  __device__ __forceinline__ void issue(int b) {
+    const int so = soff0 + min(b, nb - 1) * 8 * row_bytes;
+#pragma unroll
+    for (int i = 0; i < LPB; i++)
+      buf[b][i] = glive[i] ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, goff[i], so, 0))
+                           : u32x4_t{0, 0, 0, 0};
+  }
+
+  // the first three blocks; call before staging the activations so their latency overlaps
+  __device__ __forceinline__ void start() {
+    issue(0);
+    if constexpr (NB > 1) issue(1);
+    if constexpr (NB > 2) issue(2);
+  }
+
+  // ap: the lane's A fragment for tile row 0 (step: 4 half4 per tile row).  Returns the 16 x 16 fp32 C tile slice
+  // (lane l: rows 4(l/16)..+3, column l%16).
+  __device__ __forceinline__ float4_t run(const half4_t* ap) {
+    float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      uint8_t* st = stage + (b & 1) * STAGE;
+#pragma unroll
+      for (int i = 0; i < LPB; i++)
+        if (glive[i]) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
+      if (b + 3 < NB) issue(b + 3);
+      const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const half4_t bv = decode_group<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
+        if (u & 1)
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc1, 0, 0, 0);
+        else
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc0, 0, 0, 0);
+      }
+    }
+    return acc0 + acc1;
+  }
+};
+
+// A-operand staging in LDS: position p of the k-range, row m -> [m][p/16][q][e] with r = p % 16, q = (r & 7) >> 1,
+// e = (r & 1) | (r >> 3) << 1, rows mstride halves apart.  Lane (m, q) then reads its 4 activations for a tile as one
+// 8-byte word, in the row order 2q, 2q+1, 2q+8, 2q+9 the decoded group uses, at a 32-byte step per tile row;
+// mstride = 16 * tile rows + 4 keeps the 16 rows of a read in distinct banks.
+__device__ __forceinline__ int a_slot(int p, int m, int mstride) {
+  const int r = p & 15;
+  return m * mstride + ((p >> 4) << 4) + (((r & 7) >> 1) << 2) + ((r & 1) | ((r >> 3) << 1));
+}
+
+}  // namespace exl3

@@ -6,6 +6,8 @@ Nothing here computes on the CPU: a missing library raises ExtensionMissing.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -14,6 +16,7 @@ CODEBOOK_ID = {"3inst": 0, "mcg": 1, "mul1": 2}
 
 _workspace: dict[int, torch.Tensor] = {}
 _prefill_ws: dict[int, torch.Tensor] = {}
+_moe_ws: dict[int, torch.Tensor] = {}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -190,3 +193,45 @@ def linear_prefill(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch
                                        int(codebook), out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(),
                                        ws.numel(), _stream(x.device)), "linear_prefill")
     return out.view(*x.shape[:-1], n_total)
+
+
+MOE_TENSORS = ("gate_trellis", "up_trellis", "down_trellis", "gate_suh", "gate_svh", "up_suh", "up_svh", "down_suh",
+               "down_svh")
+
+
+def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, experts: dict[str, torch.Tensor],
+                codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed SiLU-gated EXL3 MoE layer (cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294).
+    x fp16|bf16 [T, H]; topk_ids [T, top_k] (int32 or int64); topk_weights fp32 [T, top_k]; `experts` holds the
+    stacked tensors named in MOE_TENSORS (trellis int16 [E, k/16, n/16, 16K], scales fp16 [E, k] / [E, n])."""
+    if x.dtype not in (torch.float16, torch.bfloat16) or x.dim() != 2:
+        raise ValueError("x must be a 2-D fp16/bf16 tensor")
+    T, H = x.shape
+    gt, dt = experts["gate_trellis"], experts["down_trellis"]
+    if gt.dim() != 4 or dt.dim() != 4 or gt.dtype != torch.int16:
+        raise ValueError("stacked trellis tensors must be int16 [E, k/16, n/16, 16K]")
+    E, I, K = gt.shape[0], gt.shape[2] * 16, gt.shape[3] // 16
+    if gt.shape[1] * 16 != H or tuple(dt.shape[1:3]) != (I // 16, H // 16) or dt.shape[3] != 16 * K:
+        raise ValueError(f"expert shapes {tuple(gt.shape)} / {tuple(dt.shape)} do not match H = {H}")
+    for name in MOE_TENSORS:
+        t = experts[name]
+        if not (t.is_cuda and t.is_contiguous()) or t.shape[0] != E:
+            raise ValueError(f"{name} must be a contiguous CUDA tensor with {E} experts")
+    top_k = topk_ids.shape[1]
+    ids = topk_ids.to(torch.int32).contiguous()
+    w = topk_weights.to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty((T, H), dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    need = lib.exl3_moe_workspace_bytes(T, top_k, E, H, I, K)
+    idx = x.device.index if x.device.index is not None else torch.cuda.current_device()
+    ws = _moe_ws.get(idx)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
+        _moe_ws[idx] = ws
+    wts = _lib.Exl3MoeWeights(*[experts[n].data_ptr() for n in MOE_TENSORS])
+    _lib.check(lib.exl3_moe_forward(x.contiguous().data_ptr(), int(x.dtype == torch.bfloat16), T, H, ids.data_ptr(),
+                                    w.data_ptr(), top_k, E, I, ctypes.byref(wts), K, int(codebook), out.data_ptr(),
+                                    int(out.dtype == torch.bfloat16), ws.data_ptr(), ws.numel(), _stream(x.device)),
+               "moe_forward")
+    return out
