@@ -124,6 +124,26 @@ int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const vo
                      int top_k, int num_experts, int inter, const exl3_moe_weights* weights_host, int K, int codebook,
                      void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- Quantized-KV paged decode attention (subsystem 5b) ------------------------------------------------------------ */
+/* The reference has no quantized-KV decode kernel: its nearest relative is the paged fp8 gather + dequant + blockwise
+ * fp16 attention with log-sum-exp merge of xpu/exl3xpu/fp8kv_prefill.py:73-117 (gather_dequant, prefill_attention).
+ * Cache (this library's layout): k_cache / v_cache int8 codes [num_pages][Hkv][16][128] (bits = 8) or packed uint8
+ * [num_pages][Hkv][16][64] (bits = 4: element 2i in the low nibble, 2i+1 in the high nibble, two's complement);
+ * k_scale / v_scale fp16 [num_pages][Hkv]; value = code * scale. */
+
+/* Workspace bytes of exl3_kv_decode_attention (fp32 partial (m, l, O) per chunk of pages).  No zero-fill needed. */
+size_t exl3_kv_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_pages);
+/* out[b][h] = softmax(sm_scale * q[b][h] . K_b^T) V_b over the first seq_lens[b] tokens of sequence b, whose pages are
+ * page_table[b][0 .. ceil(seq_lens[b] / 16)); query head h reads KV head h / (Hq / Hkv) (Hq / Hkv <= 16).
+ * q fp16 [B][Hq][128], page_table int32 [B][max_pages], seq_lens int32 [B], out fp16 [B][Hq][128].  A sequence of
+ * length 0 gives zeros; page ids outside [0, num_pages) are clamped (never read outside the cache).  head_dim must be
+ * 128 and page_size 16.  Two launches (split-KV over page chunks, then the log-sum-exp merge); deterministic. */
+int exl3_kv_decode_attention(const void* q, const void* k_cache, const void* v_cache, const void* k_scale,
+                             const void* v_scale, int num_pages, const void* page_table, int max_pages,
+                             const void* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                             int page_size, int bits, float sm_scale, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

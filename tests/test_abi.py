@@ -41,6 +41,16 @@ def test_workspace_size_is_deterministic_and_zero_for_bad_shapes(lib):
     (lambda l: l.exl3_had_in_group(1, 0, 4, 128, 1, 5, 1, None), "shards = 5"),
     (lambda l: l.exl3_had_out_into(1, 4, 128, 1, 1, 0, 64, 0, None), "ld_out"),
     (lambda l: l.exl3_gemm_rotated(1, 4, 128, 1, 100, 3, 1, 1, 1, 1 << 20, None), "n = 100"),
+    (lambda l: l.exl3_kv_decode_attention(1, 1, 1, 1, 1, 4, 1, 4, 1, 2, 40, 8, 64, 16, 8, 0.1, 1, 1, 1 << 20, None),
+     "head_dim = 64"),
+    (lambda l: l.exl3_kv_decode_attention(1, 1, 1, 1, 1, 4, 1, 4, 1, 2, 40, 8, 128, 16, 3, 0.1, 1, 1, 1 << 20, None),
+     "bits = 3"),
+    (lambda l: l.exl3_kv_decode_attention(1, 1, 1, 1, 1, 4, 1, 4, 1, 2, 40, 2, 128, 16, 8, 0.1, 1, 1, 1 << 20, None),
+     "group <= 16"),
+    (lambda l: l.exl3_kv_decode_attention(1, 1, 1, 1, 1, 4, 1, 4, 1, 2, 40, 8, 128, 16, 8, 0.1, 1, 1, 8, None),
+     "workspace"),
+    (lambda l: l.exl3_kv_decode_attention(1, None, 1, 1, 1, 4, 1, 4, 1, 2, 40, 8, 128, 16, 8, 0.1, 1, 1, 1 << 20,
+                                          None), "null"),
 ])
 def test_invalid_arguments_are_rejected_without_launching(lib, call, msg):
     assert call(lib) == _lib.EXL3_ERR_INVALID

@@ -1,0 +1,139 @@
+"""GPU parity of the quantized-KV paged decode attention (exl3_kv_decode_attention) against the oracle's float64
+closed form (oracle.kv_decode_attention: dequantize code * scale, softmax attention per query head).
+
+The reference has no quantized-KV decode kernel (its nearest relative is the paged fp8 attention with log-sum-exp merge
+of xpu/exl3xpu/fp8kv_prefill.py:73-117), so this path is "parity unpinned" against the reference itself; the oracle
+is pinned by tests/test_oracle.py against a contiguous-cache evaluation.  Bar: norm-rel and max-rel (max abs error over
+max |ref|) <= 2e-3 -- the kernel's own roundings are the fp16 probabilities (p * v_scale) and the fp16 output."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import exl3_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+D, PAGE = 128, 16
+
+
+def _cache(rng, num_pages, Hkv, bits):
+    kf = rng.standard_normal((num_pages, Hkv, PAGE, D)).astype(np.float16)
+    vf = rng.standard_normal((num_pages, Hkv, PAGE, D)).astype(np.float16)
+    kq, ks = orc.kv_quantize(kf, bits)
+    vq, vs = orc.kv_quantize(vf, bits)
+    if bits == 4:
+        return orc.kv_pack4(kq), orc.kv_pack4(vq), ks, vs
+    return kq, vq, ks, vs
+
+
+def _table(rng, lens, max_pages, num_pages):
+    """Each sequence gets distinct physical pages in a random order; unused entries hold -1 (never read)."""
+    perm = rng.permutation(num_pages)
+    table = np.full((len(lens), max_pages), -1, dtype=np.int32)
+    off = 0
+    for b, L in enumerate(lens):
+        n = -(-L // PAGE)
+        table[b, :n] = perm[off:off + n]
+        off += n
+    assert off <= num_pages
+    return table
+
+
+def _run(q, kc, vc, ks, vs, table, lens, bits, sm_scale):
+    from trellis_serve_amd import ops
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return ops.kv_decode_attention(t(q), t(kc), t(vc), t(ks), t(vs), t(table), t(np.asarray(lens, np.int32)), bits,
+                                   sm_scale)
+
+
+def _errs(y, ref):
+    y = y.astype(np.float64)
+    return np.linalg.norm(y - ref) / np.linalg.norm(ref), np.abs(y - ref).max() / np.abs(ref).max()
+
+
+def _case(seed, lens, Hq, Hkv, bits, max_pages=None, extra_pages=3):
+    rng = np.random.default_rng(seed)
+    npg = sum(-(-L // PAGE) for L in lens)
+    num_pages = npg + extra_pages
+    max_pages = max_pages or max(1, max(-(-L // PAGE) for L in lens))
+    kc, vc, ks, vs = _cache(rng, num_pages, Hkv, bits)
+    table = _table(rng, lens, max_pages, num_pages)
+    q = rng.standard_normal((len(lens), Hq, D)).astype(np.float16)
+    return q, kc, vc, ks, vs, table
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("lens,Hq,Hkv", [([1, 17, 300], 40, 8), ([16, 33, 1000, 64], 8, 8), ([255, 4], 32, 2),
+                                         ([2049], 40, 8)])
+def test_kv_decode_matches_closed_form(bits, lens, Hq, Hkv):
+    q, kc, vc, ks, vs, table = _case(7 + len(lens) + bits, lens, Hq, Hkv, bits)
+    sm = D ** -0.5
+    y = _run(q, kc, vc, ks, vs, table, lens, bits, sm).cpu().numpy()
+    ref = orc.kv_decode_attention(q, kc, vc, ks, vs, table, np.asarray(lens, np.int32), bits, sm)
+    nrel, mrel = _errs(y, ref)
+    print(f"bits={bits} lens={lens} heads {Hq}/{Hkv}: norm-rel {nrel:.2e} max-rel {mrel:.2e}")
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_kv_decode_c5_4k_batch16(bits):
+    """The measured configuration at 4k context: B = 16, 40 / 8 heads, random page order."""
+    lens = [4096] * 15 + [4000]
+    q, kc, vc, ks, vs, table = _case(40 + bits, lens, 40, 8, bits, extra_pages=0)
+    sm = D ** -0.5
+    y = _run(q, kc, vc, ks, vs, table, lens, bits, sm).cpu().numpy()
+    ref = orc.kv_decode_attention(q, kc, vc, ks, vs, table, np.asarray(lens, np.int32), bits, sm)
+    nrel, mrel = _errs(y, ref)
+    print(f"C5 4k bits={bits}: norm-rel {nrel:.2e} max-rel {mrel:.2e}")
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+
+
+def test_kv_decode_32k():
+    lens = [32768, 32768 - 5]
+    q, kc, vc, ks, vs, table = _case(32, lens, 40, 8, 8, extra_pages=0)
+    # a sharp query: logits of a few keys dominate (the running max moves across chunks)
+    q = (q.astype(np.float32) * 4).astype(np.float16)
+    sm = D ** -0.5
+    y = _run(q, kc, vc, ks, vs, table, lens, 8, sm).cpu().numpy()
+    ref = orc.kv_decode_attention(q, kc, vc, ks, vs, table, np.asarray(lens, np.int32), 8, sm)
+    nrel, mrel = _errs(y, ref)
+    print(f"32k: norm-rel {nrel:.2e} max-rel {mrel:.2e}")
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_kv_decode_uniform_keys_give_mean_of_values(bits):
+    """All-zero K codes: every logit is 0, so each head's output is the plain mean of its V rows (closed form)."""
+    lens = [50, 16, 1]
+    q, kc, vc, ks, vs, table = _case(5, lens, 16, 4, bits)
+    kc[:] = 0
+    y = _run(q, kc, vc, ks, vs, table, lens, bits, 0.1).cpu().numpy().astype(np.float64)
+    vcodes = orc.kv_unpack4(vc) if bits == 4 else vc
+    for b, L in enumerate(lens):
+        pages = table[b, :-(-L // PAGE)]
+        vals = (vcodes[pages].astype(np.float32) * vs[pages].astype(np.float32)[:, :, None, None])  # [n, Hkv, 16, D]
+        vals = vals.transpose(1, 0, 2, 3).reshape(4, -1, D)[:, :L].astype(np.float64)
+        mean = vals.mean(axis=1)
+        for h in range(16):
+            np.testing.assert_allclose(y[b, h], mean[h // 4], rtol=2e-3, atol=2e-3 * np.abs(mean).max())
+
+
+def test_kv_decode_page_order_and_padding_invariance():
+    """Moving a sequence's pages to other physical slots, and widening the page table, changes nothing (bit-exact);
+    a zero-length sequence gives zeros; repeated calls are bit-identical."""
+    lens = [700, 0, 129]
+    q, kc, vc, ks, vs, table = _case(11, lens, 40, 8, 8, max_pages=44, extra_pages=60)
+    first = _run(q, kc, vc, ks, vs, table, lens, 8, 0.08)
+    rng = np.random.default_rng(3)
+    P = kc.shape[0]
+    perm = rng.permutation(P)          # physical page p moves to slot perm[p]
+    kc2, vc2, ks2, vs2 = (np.empty_like(a) for a in (kc, vc, ks, vs))
+    for a2, a in ((kc2, kc), (vc2, vc), (ks2, ks), (vs2, vs)):
+        a2[perm] = a
+    table2 = np.where(table >= 0, perm[np.maximum(table, 0)], -1).astype(np.int32)
+    table2 = np.concatenate([table2, np.full((3, 20), -1, np.int32)], axis=1)
+    second = _run(q, kc2, vc2, ks2, vs2, table2, lens, 8, 0.08)
+    assert torch.equal(first[0], second[0]) and torch.equal(first[2], second[2])
+    assert not first[1].any() and not second[1].any()
+    for _ in range(3):
+        assert torch.equal(_run(q, kc, vc, ks, vs, table, lens, 8, 0.08), first)

@@ -1,0 +1,387 @@
+// Paged quantized-KV decode attention on gfx950 (one query token per sequence, GQA).
+//
+// Cache layout (this build's; the reference has no quantized-KV decode kernel -- its nearest relative is the paged
+// fp8 gather + blockwise attention with log-sum-exp merge of xpu/exl3xpu/fp8kv_prefill.py:73-117):
+//   k_cache, v_cache: 8-bit int8 [pages][Hkv][16][D], or 4-bit packed uint8 [pages][Hkv][16][D/2] (element 2i in
+//                     the low nibble, 2i+1 in the high nibble, two's complement);
+//   k_scale, v_scale: fp16 [pages][Hkv]; value = code * scale;
+//   page_table int32 [B][max_pages]; seq_lens int32 [B]; q fp16 [B][Hq][D]; out fp16 [B][Hq][D]; D = 128.
+//   Query head h reads KV head h / (Hq / Hkv).
+//
+// kv_decode_kernel: grid (chunks of chunk_pages pages, Hkv, B), 4 waves.  Wave w takes pages w, w+4, ... of its
+// workgroup's chunk, with the next page's codes in flight while it works on the current one, and keeps an online
+// softmax for the G = Hq/Hkv query heads (G <= 16; MFMA columns G..15 are idle).  Per 16-token page -- exactly one
+// 16-wide MFMA block, so the page's two scales are wave-uniform:
+//   S^T = K Q^T     4 x MFMA 16x16x32 f16.  A = the page's 16 keys (lane: key l%16, 32 dims), B = Q^T (lane: query
+//                   l%16, the same 32 dims in the same order; loaded once).  C lane: query l%16, keys 4(l/16)..+3;
+//   P^T             that C layout is already the B operand of the next MFMA; P' = p * v_scale rounded to fp16;
+//   O^T += V^T P^T  8 x MFMA 16x16x16 f16.  A = V^T (lane: dim 8(l%16) + db for block db, keys 4(l/16)..+3): the
+//                   lane loads 8 bytes of each of its 4 keys and transposes the 4 x 4 byte blocks with v_perm.
+//                   C lane: dims 32(l/16) .. +31 of query l%16 over the 8 blocks.
+// Codes become fp16 exactly: code + bias (one xor) as the low byte under 0x64 is the fp16 1024 + code + bias, and one
+// packed fp16 subtract of 1024 + bias leaves the code (integers of magnitude <= 128 are exact in fp16).  The four
+// waves merge their (m, l, O) in LDS; the workgroup writes its chunk's partial state and kv_merge_kernel combines the
+// chunks by log-sum-exp, in chunk order (deterministic).  Logits are kept in the base-2 domain (scale * log2 e).
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "exl3_api.hpp"
+#include "exl3_device.hpp"
+
+namespace exl3 {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t kv_u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t kv_u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kKvWaves = 4;
+constexpr int kHeadDim = 128;
+constexpr int kPage = 16;
+constexpr int kMaxGroup = 16;
+
+// 4 biased code bytes -> 4 fp16 (1024 + byte - sub); the fp16 subtract is exact for the code range
+__device__ __forceinline__ half4_t codes_f16(uint32_t u, _Float16 sub) {
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x05010400u);  // bytes: u0, 0x64, u1, 0x64
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x05030402u);  // bytes: u2, 0x64, u3, 0x64
+  return __builtin_bit_cast(half4_t, kv_u32x2_t{lo, hi}) - half4_t{sub, sub, sub, sub};
+}
+
+// 4 x 4 byte transpose: in[i] holds bytes 0..3 of row i; out[j] holds byte j of rows 0..3 (row order)
+__device__ __forceinline__ void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
+  const uint32_t a = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // r0b0 r1b0 r0b1 r1b1
+  const uint32_t b = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);  // r2b0 r3b0 r2b1 r3b1
+  const uint32_t c = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // r0b2 r1b2 r0b3 r1b3
+  const uint32_t d = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);  // r2b2 r3b2 r2b3 r3b3
+  out[0] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(d, c, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(d, c, 0x07060302u);
+}
+
+// reductions over the 4 lanes l, l^16, l^32, l^48 (the 16 keys of a page for one query): v_permlane16_swap and
+// v_permlane32_swap with both operands x return (x of row r, x of row r^1) and (x of half h, x of half h^1)
+__device__ __forceinline__ float max_over_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Keeps the loads above it issued here: otherwise they are free to sink to their first use, which turns the
+// next-page prefetch into a load-and-wait.  Registers are not touched, so no wait is implied.  (The cache pointers
+// carry no __restrict__: loads of restrict read-only memory count as invariant and would cross the fence.)
+__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+
+// The codes one lane needs from one (page, kv head) block, and the block's scales.
+template <int BITS>
+struct KvRegs {
+  static constexpr int ROW = BITS == 8 ? kHeadDim : kHeadDim / 2;  // bytes per token row
+  static constexpr int KW = BITS == 8 ? 8 : 4;                      // K dwords per lane
+  static constexpr int VW = BITS == 8 ? 8 : 4;                      // V dwords per lane
+  uint32_t k[KW], v[VW];
+  _Float16 ks, vs;
+
+  // lane (n, g): K row n, bytes [ROW/4 * g, +ROW/4); V rows 4g .. 4g+3, bytes [ROW/16 * n, +ROW/16)
+  __device__ __forceinline__ void load(const uint8_t* kblk, const uint8_t* vblk, const _Float16* ksc,
+                                       const _Float16* vsc, size_t bi, int n, int g) {
+    const kv_u32x4_t* kp = reinterpret_cast<const kv_u32x4_t*>(kblk + n * ROW + (ROW / 4) * g);
+    if constexpr (BITS == 8) {
+      const kv_u32x4_t a = kp[0], b = kp[1];
+      k[0] = a.x, k[1] = a.y, k[2] = a.z, k[3] = a.w, k[4] = b.x, k[5] = b.y, k[6] = b.z, k[7] = b.w;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const kv_u32x2_t t = *reinterpret_cast<const kv_u32x2_t*>(vblk + (4 * g + i) * ROW + 8 * n);
+        v[i] = t.x, v[4 + i] = t.y;
+      }
+    } else {
+      const kv_u32x4_t a = kp[0];
+      k[0] = a.x, k[1] = a.y, k[2] = a.z, k[3] = a.w;
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = *reinterpret_cast<const uint32_t*>(vblk + (4 * g + i) * ROW + 4 * n);
+    }
+    ks = ksc[bi];
+    vs = vsc[bi];
+  }
+
+  // K fragment c (dims of lane group g in the order the Q fragment uses)
+  __device__ __forceinline__ half8_t kfrag(int c) const {
+    half4_t x, y;
+    if constexpr (BITS == 8) {  // dwords 2c, 2c+1: dims 32g + 8c .. +7
+      x = codes_f16(k[2 * c] ^ 0x80808080u, (_Float16)1152.0f);
+      y = codes_f16(k[2 * c + 1] ^ 0x80808080u, (_Float16)1152.0f);
+    } else {  // dword c: low nibbles = dims 32g + 8c + {0,2,4,6}, high nibbles = +{1,3,5,7}
+      x = codes_f16((k[c] & 0x0F0F0F0Fu) ^ 0x08080808u, (_Float16)1032.0f);
+      y = codes_f16(((k[c] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u, (_Float16)1032.0f);
+    }
+    return half8_t{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+  }
+
+  // V^T fragments: vt[db] = the 4 keys' biased codes at dim 8n + db
+  __device__ __forceinline__ void vtrans(uint32_t vt[8]) const {
+    if constexpr (BITS == 8) {
+      uint32_t lo[4] = {v[0] ^ 0x80808080u, v[1] ^ 0x80808080u, v[2] ^ 0x80808080u, v[3] ^ 0x80808080u};
+      uint32_t hi[4] = {v[4] ^ 0x80808080u, v[5] ^ 0x80808080u, v[6] ^ 0x80808080u, v[7] ^ 0x80808080u};
+      transpose4x4(lo, vt);
+      transpose4x4(hi, vt + 4);
+    } else {
+      uint32_t tb[4];
+      transpose4x4(v, tb);  // tb[j]: byte j (dims 8n + 2j, 8n + 2j + 1) of the 4 keys
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        vt[2 * j] = (tb[j] & 0x0F0F0F0Fu) ^ 0x08080808u;
+        vt[2 * j + 1] = ((tb[j] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;
+      }
+    }
+  }
+};
+
+template <int BITS>
+struct KvState {
+  float m = -INFINITY, l = 0.f;  // running max (base 2) and sum for query n
+  float4_t o[8];
+
+  __device__ __forceinline__ void process(const KvRegs<BITS>& r, const half8_t qf[4], int key0, int L, float qk_scale,
+                                          int g) {
+    constexpr float kSub = BITS == 8 ? 1152.0f : 1032.0f;
+    float4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; c++) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.kfrag(c), qf[c], st, 0, 0, 0);
+    const float sc = (float)r.ks * qk_scale;
+    float sv[4], pmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      sv[i] = key0 + 4 * g + i < L ? st[i] * sc : -INFINITY;
+      pmax = fmaxf(pmax, sv[i]);
+    }
+    const float m_new = fmaxf(m, max_over_groups(pmax));
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first page
+    m = m_new;
+    const float vs = (float)r.vs;
+    float psum = 0.f;
+    half4_t pf;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float p = __builtin_amdgcn_exp2f(sv[i] - m_new);
+      psum += p;
+      pf[i] = (_Float16)(p * vs);
+    }
+    l = l * alpha + sum_over_groups(psum);
+    uint32_t vt[8];
+    r.vtrans(vt);
+#pragma unroll
+    for (int db = 0; db < 8; db++)
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(codes_f16(vt[db], (_Float16)kSub), pf, o[db] * alpha, 0, 0, 0);
+  }
+};
+
+template <int BITS>
+__global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
+    const _Float16* __restrict__ q, const uint8_t* kc, const uint8_t* vc, const _Float16* ksc, const _Float16* vsc,
+    int num_pages,
+    const int* __restrict__ page_table, int max_pages, const int* __restrict__ seq_lens, int Hq, int Hkv,
+    float qk_scale, int chunk_pages, float* __restrict__ part_o, float* __restrict__ part_ml) {
+  constexpr int ROW = KvRegs<BITS>::ROW;
+  extern __shared__ float red[];  // [4 waves][G][D + 1] then [4 waves][G][2]
+  const int chunk = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int G = Hq / Hkv;
+  const int L = min(seq_lens[b], max_pages * kPage);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  const int n = l & 15, g = l >> 4;
+
+  // Q^T fragment of query n (zero for n >= G), dims in K-fragment order
+  half8_t qf[4];
+  {
+    const _Float16* qrow = q + ((size_t)b * Hq + hk * G + min(n, G - 1)) * kHeadDim + 32 * g;
+    const _Float16 live = n < G ? (_Float16)1.0f : (_Float16)0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int d = BITS == 8 ? 8 * c + e : 8 * c + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
+        qf[c][e] = qrow[d] * live;
+      }
+  }
+
+  KvState<BITS> s;
+#pragma unroll
+  for (int db = 0; db < 8; db++) s.o[db] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // this wave's pages: logical pages p0 + w, p0 + w + 4, ... below min(chunk end, pages of the sequence)
+  const int p0 = chunk * chunk_pages;
+  const int p_end = min(p0 + chunk_pages, (L + kPage - 1) / kPage);
+  const int* ptab = page_table + (size_t)b * max_pages;
+  const size_t blk_bytes = (size_t)kPage * ROW;
+  int lp = p0 + w;
+  if (lp < p_end) {
+    KvRegs<BITS> ra, rb;
+    // out-of-range page ids are clamped into the cache (never dereferenced outside it)
+    auto page_of = [&](int p) { return (size_t)min(max(ptab[p], 0), num_pages - 1) * Hkv + hk; };
+    size_t bi = page_of(lp);
+    ra.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
+    while (true) {
+      // two pages per trip so the in-flight registers alternate without copies
+      bi = page_of(min(lp + kKvWaves, p_end - 1));
+      rb.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
+      issue_fence();
+      s.process(ra, qf, lp * kPage, L, qk_scale, g);
+      lp += kKvWaves;
+      if (lp >= p_end) break;
+      bi = page_of(min(lp + kKvWaves, p_end - 1));
+      ra.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
+      issue_fence();
+      s.process(rb, qf, lp * kPage, L, qk_scale, g);
+      lp += kKvWaves;
+      if (lp >= p_end) break;
+    }
+  }
+
+  // merge the 4 waves; lane (n, g) holds dims 32g + 8i + db (i < 4, db < 8) of query n
+  float* red_o = red;
+  float* red_ml = red + kKvWaves * G * (kHeadDim + 1);
+  if (n < G) {
+    float* dst = red_o + (w * G + n) * (kHeadDim + 1) + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int db = 0; db < 8; db++) dst[8 * i + db] = s.o[db][i];
+    if (g == 0) {
+      red_ml[(w * G + n) * 2] = s.m;
+      red_ml[(w * G + n) * 2 + 1] = s.l;
+    }
+  }
+  __syncthreads();
+  const int tq = threadIdx.x >> 4, td = (threadIdx.x & 15) * 8;  // query tq, dims td .. td+7
+  if (tq >= G) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int ww = 0; ww < kKvWaves; ww++) mx = fmaxf(mx, red_ml[(ww * G + tq) * 2]);
+  float lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ww = 0; ww < kKvWaves; ww++) {
+    const float mw = red_ml[(ww * G + tq) * 2];
+    const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
+    lsum += red_ml[(ww * G + tq) * 2 + 1] * f;
+    const float* src = red_o + (ww * G + tq) * (kHeadDim + 1) + td;
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] += src[e] * f;
+  }
+  const size_t slot = (((size_t)b * Hkv + hk) * gridDim.x + chunk) * G + tq;
+  float4_t* po = reinterpret_cast<float4_t*>(part_o + slot * kHeadDim + td);
+  po[0] = float4_t{acc[0], acc[1], acc[2], acc[3]};
+  po[1] = float4_t{acc[4], acc[5], acc[6], acc[7]};
+  if (td == 0) {
+    part_ml[slot * 2] = mx;
+    part_ml[slot * 2 + 1] = lsum;
+  }
+}
+
+// out[b][h] = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c over the chunks in order; one workgroup per (kv head, b)
+__global__ __launch_bounds__(256) void kv_merge_kernel(const float* __restrict__ part_o,
+                                                       const float* __restrict__ part_ml, int Hq, int Hkv, int chunks,
+                                                       _Float16* __restrict__ out) {
+  const int hk = blockIdx.x, b = blockIdx.y;
+  const int G = Hq / Hkv;
+  const int tq = threadIdx.x >> 4, td = (threadIdx.x & 15) * 8;
+  if (tq >= G) return;
+  const size_t base = ((size_t)b * Hkv + hk) * chunks * G + tq;
+  float mx = -INFINITY;
+  for (int c = 0; c < chunks; c++) mx = fmaxf(mx, part_ml[(base + (size_t)c * G) * 2]);
+  float lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < chunks; c++) {
+    const size_t slot = base + (size_t)c * G;
+    const float mc = part_ml[slot * 2];
+    if (mc == -INFINITY) continue;
+    const float f = __builtin_amdgcn_exp2f(mc - mx);
+    lsum += part_ml[slot * 2 + 1] * f;
+    const float4_t* po = reinterpret_cast<const float4_t*>(part_o + slot * kHeadDim + td);
+    const float4_t a = po[0], c4 = po[1];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      acc[e] += a[e] * f;
+      acc[4 + e] += c4[e] * f;
+    }
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  half8_t h;
+#pragma unroll
+  for (int e = 0; e < 8; e++) h[e] = (_Float16)(acc[e] * inv);
+  *reinterpret_cast<half8_t*>(out + ((size_t)b * Hq + hk * G + tq) * kHeadDim + td) = h;
+}
+
+// pages per workgroup: a multiple of the 4 waves, at most about 64 chunks per sequence
+static int kv_chunk_pages(int max_pages) {
+  int cp = 16;
+  if (const char* e = getenv("EXL3_KV_CHUNK_PAGES")) cp = std::max(1, atoi(e));
+  cp = std::max(cp, (max_pages + 63) / 64);
+  return (cp + kKvWaves - 1) / kKvWaves * kKvWaves;
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" size_t exl3_kv_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_pages) {
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads < num_kv_heads || max_pages <= 0) return 0;
+  const int cp = kv_chunk_pages(max_pages);
+  const size_t chunks = (max_pages + cp - 1) / cp;
+  const size_t slots = (size_t)batch * num_kv_heads * chunks * (num_q_heads / num_kv_heads);
+  return slots * (kHeadDim + 2) * sizeof(float);
+}
+
+extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, const void* v_cache, const void* k_scale,
+                                        const void* v_scale, int num_pages, const void* page_table, int max_pages,
+                                        const void* seq_lens, int batch, int num_q_heads, int num_kv_heads,
+                                        int head_dim, int page_size, int bits, float sm_scale, void* out,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  EXL3_CHECK_ARG(q && k_cache && v_cache && k_scale && v_scale && page_table && seq_lens && out,
+                 "exl3_kv_decode_attention: null pointer");
+  EXL3_CHECK_ARG(head_dim == kHeadDim && page_size == kPage,
+                 "exl3_kv_decode_attention: head_dim = %d, page_size = %d (supported: 128, 16)", head_dim, page_size);
+  EXL3_CHECK_ARG(bits == 4 || bits == 8, "exl3_kv_decode_attention: bits = %d (4 or 8)", bits);
+  EXL3_CHECK_ARG(batch >= 0 && num_pages >= 1 && max_pages >= 1 && num_kv_heads >= 1 &&
+                     num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads >= 1 &&
+                     num_q_heads / num_kv_heads <= kMaxGroup,
+                 "exl3_kv_decode_attention: batch = %d, pages = %d, max_pages = %d, heads %d / %d (group <= 16)",
+                 batch, num_pages, max_pages, num_q_heads, num_kv_heads);
+  if (batch == 0) return EXL3_OK;
+  const size_t need = exl3_kv_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, max_pages);
+  EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_kv_decode_attention: workspace %zu bytes, need %zu",
+                 workspace_bytes, need);
+  const int G = num_q_heads / num_kv_heads;
+  const int cp = kv_chunk_pages(max_pages);
+  const int chunks = (max_pages + cp - 1) / cp;
+  float* part_o = static_cast<float*>(workspace);
+  float* part_ml = part_o + (size_t)batch * num_kv_heads * chunks * G * kHeadDim;
+  const float qk_scale = sm_scale * 1.4426950408889634f;  // logits in base 2
+  const size_t lds = (size_t)kKvWaves * G * (kHeadDim + 1 + 2) * sizeof(float);
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(chunks, num_kv_heads, batch);
+  auto qp = static_cast<const _Float16*>(q);
+  auto kp = static_cast<const uint8_t*>(k_cache);
+  auto vp = static_cast<const uint8_t*>(v_cache);
+  auto ksp = static_cast<const _Float16*>(k_scale);
+  auto vsp = static_cast<const _Float16*>(v_scale);
+  auto pt = static_cast<const int*>(page_table);
+  auto sl = static_cast<const int*>(seq_lens);
+  if (bits == 8)
+    kv_decode_kernel<8><<<grid, kKvWaves * 64, lds, st>>>(qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl,
+                                                          num_q_heads, num_kv_heads, qk_scale, cp, part_o, part_ml);
+  else
+    kv_decode_kernel<4><<<grid, kKvWaves * 64, lds, st>>>(qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl,
+                                                          num_q_heads, num_kv_heads, qk_scale, cp, part_o, part_ml);
+  EXL3_CHECK_LAUNCH();
+  kv_merge_kernel<<<dim3(num_kv_heads, batch), 256, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
+                                                             static_cast<_Float16*>(out));
+  EXL3_CHECK_LAUNCH();
+  return EXL3_OK;
+}

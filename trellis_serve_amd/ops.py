@@ -17,6 +17,7 @@ CODEBOOK_ID = {"3inst": 0, "mcg": 1, "mul1": 2}
 _workspace: dict[int, torch.Tensor] = {}
 _prefill_ws: dict[int, torch.Tensor] = {}
 _moe_ws: dict[int, torch.Tensor] = {}
+_kv_ws: dict[int, torch.Tensor] = {}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -234,4 +235,53 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Ten
                                     w.data_ptr(), top_k, E, I, ctypes.byref(wts), K, int(codebook), out.data_ptr(),
                                     int(out.dtype == torch.bfloat16), ws.data_ptr(), ws.numel(), _stream(x.device)),
                "moe_forward")
+    return out
+
+
+def kv_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, k_scale: torch.Tensor,
+                        v_scale: torch.Tensor, page_table: torch.Tensor, seq_lens: torch.Tensor, bits: int,
+                        sm_scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Single-token decode attention over a quantized paged KV cache (split-KV + log-sum-exp merge; the merge follows
+    xpu/exl3xpu/fp8kv_prefill.py:85-117).  q fp16 [B, Hq, 128]; k_cache / v_cache int8 [P, Hkv, 16, 128] (bits=8)
+    or uint8 [P, Hkv, 16, 64] (bits=4, packed nibbles); k_scale / v_scale fp16 [P, Hkv]; page_table int32
+    [B, max_pages]; seq_lens int32 [B].  Returns fp16 [B, Hq, 128]."""
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    if q.dtype != torch.float16 or q.dim() != 3:
+        raise ValueError("q must be fp16 [B, Hq, D]")
+    B, Hq, D = q.shape
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache / v_cache must have the same [P, Hkv, page, row] shape")
+    P, Hkv, page, row = k_cache.shape
+    if row != (D if bits == 8 else D // 2):
+        raise ValueError(f"cache row of {row} bytes does not hold {D} {bits}-bit codes")
+    if k_cache.element_size() != 1 or v_cache.element_size() != 1:
+        raise ValueError("caches must hold 1-byte codes (int8 / uint8)")
+    for name, t in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if t.dtype != torch.float16 or tuple(t.shape) != (P, Hkv):
+            raise ValueError(f"{name} must be fp16 [{P}, {Hkv}]")
+    if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.shape[0] != B:
+        raise ValueError("page_table must be int32 [B, max_pages]")
+    if seq_lens.dtype != torch.int32 or tuple(seq_lens.shape) != (B,):
+        raise ValueError("seq_lens must be int32 [B]")
+    tensors = (q, k_cache, v_cache, k_scale, v_scale, page_table, seq_lens)
+    if not all(t.is_cuda and t.is_contiguous() for t in tensors):
+        raise ValueError("all inputs must be contiguous CUDA tensors")
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=torch.float16, device=q.device)
+    lib = _lib.load()
+    max_pages = page_table.shape[1]
+    need = lib.exl3_kv_decode_workspace_bytes(B, Hq, Hkv, max_pages)
+    idx = q.device.index if q.device.index is not None else torch.cuda.current_device()
+    ws = _kv_ws.get(idx)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)
+        _kv_ws[idx] = ws
+    _lib.check(lib.exl3_kv_decode_attention(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
+                                            v_scale.data_ptr(), P, page_table.data_ptr(), max_pages,
+                                            seq_lens.data_ptr(), B, Hq, Hkv, D, page, int(bits), float(sm_scale),
+                                            out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(q.device)),
+               "kv_decode_attention")
     return out
