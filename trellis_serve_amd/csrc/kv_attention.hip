@@ -79,7 +79,10 @@ __device__ __forceinline__ float sum_over_groups(float v) {
 // Keeps the loads above it issued here: otherwise they are free to sink to their first use, which turns the
 // next-page prefetch into a load-and-wait.  Registers are not touched, so no wait is implied.  (The cache pointers
 // carry no __restrict__: loads of restrict read-only memory count as invariant and would cross the fence.)
-__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+__device__ __forceinline__ void issue_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);  // and no instruction that waits on older loads is scheduled above them
+}
 
 // The codes one lane needs from one (page, kv head) block, and the block's scales.
 template <int BITS>
@@ -112,17 +115,22 @@ struct KvRegs {
     vs = vsc[bi];
   }
 
-  // K fragment c (dims of lane group g in the order the Q fragment uses)
+  // K fragment c, biased: 1024 + bias + code (bias 128 / 8; removed after the MFMA, per page, from the query sums).
+  // Dims of lane group g, in the order the Q fragment uses: 8 bits, dwords 2c, 2c+1 = dims 32g + 8c + 0..7;
+  // 4 bits, dword c = dims 32g + 8c + 0..7 as nibbles 0..7, taken in pairs (s, s+4) straight into fp16 halves.
   __device__ __forceinline__ half8_t kfrag(int c) const {
-    half4_t x, y;
-    if constexpr (BITS == 8) {  // dwords 2c, 2c+1: dims 32g + 8c .. +7
-      x = codes_f16(k[2 * c] ^ 0x80808080u, (_Float16)1152.0f);
-      y = codes_f16(k[2 * c + 1] ^ 0x80808080u, (_Float16)1152.0f);
-    } else {  // dword c: low nibbles = dims 32g + 8c + {0,2,4,6}, high nibbles = +{1,3,5,7}
-      x = codes_f16((k[c] & 0x0F0F0F0Fu) ^ 0x08080808u, (_Float16)1032.0f);
-      y = codes_f16(((k[c] >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u, (_Float16)1032.0f);
+    if constexpr (BITS == 8) {
+      const uint32_t x = k[2 * c] ^ 0x80808080u, y = k[2 * c + 1] ^ 0x80808080u;
+      return __builtin_bit_cast(half8_t, kv_u32x4_t{__builtin_amdgcn_perm(0x64646464u, x, 0x05010400u),
+                                                     __builtin_amdgcn_perm(0x64646464u, x, 0x05030402u),
+                                                     __builtin_amdgcn_perm(0x64646464u, y, 0x05010400u),
+                                                     __builtin_amdgcn_perm(0x64646464u, y, 0x05030402u)});
+    } else {
+      const uint32_t x = k[c];
+      return __builtin_bit_cast(half8_t, kv_u32x4_t{(x & 0x000F000Fu) ^ 0x64086408u, ((x >> 4) & 0x000F000Fu) ^ 0x64086408u,
+                                                     ((x >> 8) & 0x000F000Fu) ^ 0x64086408u,
+                                                     ((x >> 12) & 0x000F000Fu) ^ 0x64086408u});
     }
-    return half8_t{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
   }
 
   // V^T fragments: vt[db] = the 4 keys' biased codes at dim 8n + db
@@ -149,41 +157,52 @@ struct KvState {
   float m = -INFINITY, l = 0.f;  // running max (base 2) and sum for query n
   float4_t o[8];
 
-  __device__ __forceinline__ void process(const KvRegs<BITS>& r, const half8_t qf[4], int key0, int L, float qk_scale,
-                                          int g) {
-    constexpr float kSub = BITS == 8 ? 1152.0f : 1032.0f;
+  // One page: logits in base 2 are (S - kbias * qsum) * k_scale * qk_scale.  The reference max m moves only when a
+  // page max passes it by more than 4 (then every p <= 16, and P' = p * v_scale stays far inside fp16), so O and l
+  // are rarely rescaled; (m, l, O) stay consistent for the merges either way.
+  __device__ __forceinline__ void process(const KvRegs<BITS>& r, const half8_t qf[4], float qsum, int key0, int L,
+                                          float qk_scale, int g) {
+    constexpr float kBias = BITS == 8 ? 1152.0f : 1032.0f;
     float4_t st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; c++) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(r.kfrag(c), qf[c], st, 0, 0, 0);
     const float sc = (float)r.ks * qk_scale;
-    float sv[4], pmax = -INFINITY;
+    const float off = -kBias * qsum * sc;
+    float sv[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      sv[i] = key0 + 4 * g + i < L ? st[i] * sc : -INFINITY;
-      pmax = fmaxf(pmax, sv[i]);
+    for (int i = 0; i < 4; i++) sv[i] = __builtin_fmaf(st[i], sc, off);
+    if (key0 + kPage > L) {  // the sequence ends inside this page
+#pragma unroll
+      for (int i = 0; i < 4; i++) sv[i] = key0 + 4 * g + i < L ? sv[i] : -INFINITY;
     }
-    const float m_new = fmaxf(m, max_over_groups(pmax));
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first page
-    m = m_new;
+    const float pm = max_over_groups(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+    if (__builtin_amdgcn_ballot_w64(pm > m + 4.f)) {
+      const float m_new = fmaxf(m, pm);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first page (m = -inf)
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 8; db++) o[db] *= alpha;
+    }
     const float vs = (float)r.vs;
     float psum = 0.f;
     half4_t pf;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const float p = __builtin_amdgcn_exp2f(sv[i] - m_new);
+      const float p = __builtin_amdgcn_exp2f(sv[i] - m);
       psum += p;
       pf[i] = (_Float16)(p * vs);
     }
-    l = l * alpha + sum_over_groups(psum);
+    l += sum_over_groups(psum);
     uint32_t vt[8];
     r.vtrans(vt);
 #pragma unroll
     for (int db = 0; db < 8; db++)
-      o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(codes_f16(vt[db], (_Float16)kSub), pf, o[db] * alpha, 0, 0, 0);
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(codes_f16(vt[db], (_Float16)kBias), pf, o[db], 0, 0, 0);
   }
 };
 
-template <int BITS>
+template <int BITS, int DEPTH>
 __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
     const _Float16* __restrict__ q, const uint8_t* kc, const uint8_t* vc, const _Float16* ksc, const _Float16* vsc,
     int num_pages,
@@ -198,8 +217,9 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
   const int l = threadIdx.x & 63;
   const int n = l & 15, g = l >> 4;
 
-  // Q^T fragment of query n (zero for n >= G), dims in K-fragment order
+  // Q^T fragment of query n (zero for n >= G), dims in K-fragment order; qsum = sum of its 128 dims
   half8_t qf[4];
+  float qpart = 0.f;
   {
     const _Float16* qrow = q + ((size_t)b * Hq + hk * G + min(n, G - 1)) * kHeadDim + 32 * g;
     const _Float16 live = n < G ? (_Float16)1.0f : (_Float16)0.0f;
@@ -207,10 +227,12 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
     for (int c = 0; c < 4; c++)
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        const int d = BITS == 8 ? 8 * c + e : 8 * c + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
+        const int d = BITS == 8 ? 8 * c + e : 8 * c + (e >> 1) + 4 * (e & 1);
         qf[c][e] = qrow[d] * live;
+        qpart += (float)qf[c][e];
       }
   }
+  const float qsum = sum_over_groups(qpart);
 
   KvState<BITS> s;
 #pragma unroll
@@ -223,25 +245,29 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
   const size_t blk_bytes = (size_t)kPage * ROW;
   int lp = p0 + w;
   if (lp < p_end) {
-    KvRegs<BITS> ra, rb;
-    // out-of-range page ids are clamped into the cache (never dereferenced outside it)
+    // DEPTH register sets rotate: DEPTH - 1 pages are in flight while one is worked on.  The trip is unrolled over
+    // the sets so each keeps its registers (no copies that would wait on their loads).  Loads past the wave's last
+    // page repeat that page.  Out-of-range page ids are clamped into the cache (never dereferenced outside it).
+    KvRegs<BITS> r[DEPTH];
     auto page_of = [&](int p) { return (size_t)min(max(ptab[p], 0), num_pages - 1) * Hkv + hk; };
-    size_t bi = page_of(lp);
-    ra.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
-    while (true) {
-      // two pages per trip so the in-flight registers alternate without copies
-      bi = page_of(min(lp + kKvWaves, p_end - 1));
-      rb.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
-      issue_fence();
-      s.process(ra, qf, lp * kPage, L, qk_scale, g);
-      lp += kKvWaves;
-      if (lp >= p_end) break;
-      bi = page_of(min(lp + kKvWaves, p_end - 1));
-      ra.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
-      issue_fence();
-      s.process(rb, qf, lp * kPage, L, qk_scale, g);
-      lp += kKvWaves;
-      if (lp >= p_end) break;
+    auto load = [&](KvRegs<BITS>& dst, int p) {
+      const size_t bi = page_of(min(p, p_end - 1));
+      dst.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
+    };
+#pragma unroll
+    for (int j = 0; j < DEPTH - 1; j++) load(r[j], lp + j * kKvWaves);
+    bool more = true;
+    while (more) {
+#pragma unroll
+      for (int j = 0; j < DEPTH; j++) {
+        if (more) {
+          load(r[(j + DEPTH - 1) % DEPTH], lp + (DEPTH - 1) * kKvWaves);
+          issue_fence();
+          s.process(r[j], qf, qsum, lp * kPage, L, qk_scale, g);
+          lp += kKvWaves;
+          more = lp < p_end;
+        }
+      }
     }
   }
 
@@ -285,44 +311,62 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
   }
 }
 
-// out[b][h] = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c over the chunks in order; one workgroup per (kv head, b)
+// out[b][h] = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  One workgroup per query head; wave w folds chunks
+// w, w+4, ... into a running (M, L, O) (lane: dims 2l, 2l+1), then the 4 waves combine in LDS.  Fixed order.
 __global__ __launch_bounds__(256) void kv_merge_kernel(const float* __restrict__ part_o,
                                                        const float* __restrict__ part_ml, int Hq, int Hkv, int chunks,
                                                        _Float16* __restrict__ out) {
-  const int hk = blockIdx.x, b = blockIdx.y;
-  const int G = Hq / Hkv;
-  const int tq = threadIdx.x >> 4, td = (threadIdx.x & 15) * 8;
-  if (tq >= G) return;
-  const size_t base = ((size_t)b * Hkv + hk) * chunks * G + tq;
-  float mx = -INFINITY;
-  for (int c = 0; c < chunks; c++) mx = fmaxf(mx, part_ml[(base + (size_t)c * G) * 2]);
-  float lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < chunks; c++) {
-    const size_t slot = base + (size_t)c * G;
-    const float mc = part_ml[slot * 2];
-    if (mc == -INFINITY) continue;
-    const float f = __builtin_amdgcn_exp2f(mc - mx);
-    lsum += part_ml[slot * 2 + 1] * f;
-    const float4_t* po = reinterpret_cast<const float4_t*>(part_o + slot * kHeadDim + td);
-    const float4_t a = po[0], c4 = po[1];
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      acc[e] += a[e] * f;
-      acc[4 + e] += c4[e] * f;
-    }
+  __shared__ float sm_ml[kKvWaves][2];
+  __shared__ float sm_o[kKvWaves][kHeadDim];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int G = Hq / Hkv, hk = h / G, q = h - hk * G;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
+  const size_t base = ((size_t)b * Hkv + hk) * chunks;  // slot of chunk c: (base + c) * G + q
+  float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
+  for (int c = w; c < chunks; c += kKvWaves) {
+    const size_t slot = (base + c) * G + q;
+    const float mc = part_ml[slot * 2], lc = part_ml[slot * 2 + 1];
+    const float2 oc = *reinterpret_cast<const float2*>(part_o + slot * kHeadDim + 2 * l);
+    const float mn = fmaxf(M, mc);
+    // equal maxima scale by 1 (also covers -inf == -inf: an empty chunk has l = 0, O = 0)
+    const float fa = M == mn ? 1.f : __builtin_amdgcn_exp2f(M - mn);
+    const float fc = mc == mn ? 1.f : __builtin_amdgcn_exp2f(mc - mn);
+    L = L * fa + lc * fc;
+    a0 = a0 * fa + oc.x * fc;
+    a1 = a1 * fa + oc.y * fc;
+    M = mn;
   }
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  half8_t h;
+  if (l == 0) {
+    sm_ml[w][0] = M;
+    sm_ml[w][1] = L;
+  }
+  sm_o[w][2 * l] = a0;
+  sm_o[w][2 * l + 1] = a1;
+  __syncthreads();
+  if (threadIdx.x >= kHeadDim) return;
+  const int d = threadIdx.x;
+  float mx = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < 8; e++) h[e] = (_Float16)(acc[e] * inv);
-  *reinterpret_cast<half8_t*>(out + ((size_t)b * Hq + hk * G + tq) * kHeadDim + td) = h;
+  for (int ww = 0; ww < kKvWaves; ww++) mx = fmaxf(mx, sm_ml[ww][0]);
+  float lsum = 0.f, acc = 0.f;
+#pragma unroll
+  for (int ww = 0; ww < kKvWaves; ww++) {
+    const float f = sm_ml[ww][0] == mx ? 1.f : __builtin_amdgcn_exp2f(sm_ml[ww][0] - mx);
+    lsum += sm_ml[ww][1] * f;
+    acc += sm_o[ww][d] * f;
+  }
+  out[((size_t)b * Hq + h) * kHeadDim + d] = (_Float16)(lsum > 0.f ? acc / lsum : 0.f);
 }
 
-// pages per workgroup: a multiple of the 4 waves, at most about 64 chunks per sequence
-static int kv_chunk_pages(int max_pages) {
-  int cp = 16;
-  if (const char* e = getenv("EXL3_KV_CHUNK_PAGES")) cp = std::max(1, atoi(e));
-  cp = std::max(cp, (max_pages + 63) / 64);
+// Pages per workgroup: the chunks of all (sequence, kv head) pairs should fill the GPU about `target` workgroups
+// deep (fewer chunks mean fewer partial states to write and merge); a multiple of the 4 waves.
+static int kv_chunk_pages(int batch, int num_kv_heads, int max_pages) {
+  int target = 1024;
+  if (const char* e = getenv("EXL3_KV_TARGET_WGS")) target = std::max(1, atoi(e));
+  const long pairs = (long)batch * num_kv_heads;
+  const long chunks = std::max(1L, std::min((long)(max_pages + kKvWaves - 1) / kKvWaves, (target + pairs - 1) / pairs));
+  const int cp = (int)((max_pages + chunks - 1) / chunks);
   return (cp + kKvWaves - 1) / kKvWaves * kKvWaves;
 }
 
@@ -332,7 +376,7 @@ using namespace exl3;
 
 extern "C" size_t exl3_kv_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_pages) {
   if (batch <= 0 || num_kv_heads <= 0 || num_q_heads < num_kv_heads || max_pages <= 0) return 0;
-  const int cp = kv_chunk_pages(max_pages);
+  const int cp = kv_chunk_pages(batch, num_kv_heads, max_pages);
   const size_t chunks = (max_pages + cp - 1) / cp;
   const size_t slots = (size_t)batch * num_kv_heads * chunks * (num_q_heads / num_kv_heads);
   return slots * (kHeadDim + 2) * sizeof(float);
@@ -358,7 +402,7 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_kv_decode_attention: workspace %zu bytes, need %zu",
                  workspace_bytes, need);
   const int G = num_q_heads / num_kv_heads;
-  const int cp = kv_chunk_pages(max_pages);
+  const int cp = kv_chunk_pages(batch, num_kv_heads, max_pages);
   const int chunks = (max_pages + cp - 1) / cp;
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)batch * num_kv_heads * chunks * G * kHeadDim;
@@ -373,14 +417,18 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
   auto vsp = static_cast<const _Float16*>(v_scale);
   auto pt = static_cast<const int*>(page_table);
   auto sl = static_cast<const int*>(seq_lens);
-  if (bits == 8)
-    kv_decode_kernel<8><<<grid, kKvWaves * 64, lds, st>>>(qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl,
-                                                          num_q_heads, num_kv_heads, qk_scale, cp, part_o, part_ml);
-  else
-    kv_decode_kernel<4><<<grid, kKvWaves * 64, lds, st>>>(qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl,
-                                                          num_q_heads, num_kv_heads, qk_scale, cp, part_o, part_ml);
+  int depth = 2;  // register page sets per wave (prefetch distance + 1); deeper sets measured no faster
+  if (const char* e = getenv("EXL3_KV_DEPTH")) depth = std::min(5, std::max(2, atoi(e)));
+  using Kern = decltype(&kv_decode_kernel<8, 2>);
+  static const Kern table[2][4] = {{kv_decode_kernel<4, 2>, kv_decode_kernel<4, 3>, kv_decode_kernel<4, 4>,
+                                    kv_decode_kernel<4, 5>},
+                                   {kv_decode_kernel<8, 2>, kv_decode_kernel<8, 3>, kv_decode_kernel<8, 4>,
+                                    kv_decode_kernel<8, 5>}};
+  table[bits == 8][depth - 2]<<<grid, kKvWaves * 64, lds, st>>>(qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl,
+                                                                num_q_heads, num_kv_heads, qk_scale, cp, part_o,
+                                                                part_ml);
   EXL3_CHECK_LAUNCH();
-  kv_merge_kernel<<<dim3(num_kv_heads, batch), 256, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
+  kv_merge_kernel<<<dim3(num_q_heads, batch), 256, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
                                                              static_cast<_Float16*>(out));
   EXL3_CHECK_LAUNCH();
   return EXL3_OK;
