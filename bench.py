@@ -10,8 +10,9 @@ before timing starts; R rotating copies of the layer set (>= 512 MB, twice the 2
 
 Prints one JSON line: metric/value = algorithmic HBM GB/s of the layer set at M = 1 (trellis + sign vectors +
 activations in/out, BASELINE.md C2 = 128,174,080 B per step), plus the roofline of the dominant kernel (the fused
-decode-GEMV), the CPU baseline (the numpy oracle, 1 core, on a bounded sample), the M = 4 / 16 rates and the prefill
-decode-GEMM rate when that path is present.
+decode-GEMV), the CPU baseline (the numpy oracle, 1 core, on a bounded sample), the M = 4 / 16 rates, and the other
+configs as reported fields: the prefill decode-GEMM TFLOPS (configs[2], `decode_gemm_tflops_m2048` is the second half
+of the metric), the MoE layer and the quantized-KV decode attention.
 """
 from __future__ import annotations
 
@@ -139,6 +140,121 @@ def cpu_baseline(seconds_target: float = 15.0) -> dict:
 
 
 DOMINANT = "gate_up"  # the largest fused linear: its gemv_kernel instance is the dominant kernel of a step
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def _graph_us(torch, fn, calls: int, reps: int = 3) -> float:
+    """Mean device time of fn() in microseconds: a graph of `calls` back-to-back calls, replayed `reps` times."""
+    g = _capture(torch, lambda: [fn(i) for i in range(calls)])
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (calls * reps)
+
+
+def bench_prefill(torch, ops, dev) -> dict:
+    """one 5120 -> 17408 linear, fp16 x ~ N(0,1) * 0.5, the fused decode-GEMM
+    (exl3_linear_prefill).  M in {512, 2048, 8192} at K = 3 MCG, and M = 2048 over K in {2,4,5,6,8} cycling the three
+    codebooks.  TFLOPS = 2 M k n / device time."""
+    k, n = 5120, 17408
+    g = torch.Generator(device="cpu").manual_seed(11)
+    cases = [(3, 1, 512), (3, 1, 2048), (3, 1, 8192), (2, 0, 2048), (4, 2, 2048), (5, 1, 2048), (6, 0, 2048),
+             (8, 2, 2048)]
+    names = {0: "3inst", 1: "mcg", 2: "mul1"}
+    out = {}
+    for K, cb, M in cases:
+        tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, generator=g).to(dev)
+        suh = (torch.randint(0, 2, (k,), generator=g) * 2 - 1).half().to(dev)
+        svh = (torch.randint(0, 2, (n,), generator=g) * 2 - 1).half().to(dev)
+        x = (torch.randn((M, k), generator=g) * 0.5).half().to(dev)
+        y = torch.empty((M, n), dtype=torch.float16, device=dev)
+        us = _graph_us(torch, lambda i: ops.linear_prefill(x, [tr], [suh], [svh], cb, out=y), 5)
+        tf = 2.0 * M * k * n / (us * 1e-6) / 1e12
+        out[f"K{K}_{names[cb]}_M{M}"] = {"us": round(us, 1), "TFLOPS": round(tf, 1),
+                                        "pct_mfma_peak": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 2)}
+        print(f"[bench] prefill K={K} {names[cb]} M={M}: {us:.1f} us, {tf:.0f} TFLOPS", file=sys.stderr, flush=True)
+    return out
+
+
+def bench_moe(torch, ops, dev) -> dict:
+    """128 experts, top-8, hidden 2048, intermediate 768, K = 3 MCG; router logits fp32 N(0,1),
+    top-8 ids and softmax weights over the selected logits.  Three rotating copies of the experts, a new routing per
+    call.  Bytes = touched experts x 1,786,368 (trellis + sign vectors) + T x (8192 + 64)."""
+    from trellis_serve_amd.ops import MOE_TENSORS
+    E, H, I, K, top_k, copies = 128, 2048, 768, 3, 8, 3
+    g = torch.Generator(device="cpu").manual_seed(12)
+
+    def experts():
+        d = {}
+        for proj, (kk, nn) in (("gate", (H, I)), ("up", (H, I)), ("down", (I, H))):
+            d[f"{proj}_trellis"] = torch.randint(-32768, 32768, (E, kk // 16, nn // 16, 16 * K), dtype=torch.int16,
+                                                 generator=g).to(dev)
+            d[f"{proj}_suh"] = (torch.randint(0, 2, (E, kk), generator=g) * 2 - 1).half().to(dev)
+            d[f"{proj}_svh"] = (torch.randint(0, 2, (E, nn), generator=g) * 2 - 1).half().to(dev)
+        assert set(d) == set(MOE_TENSORS)
+        return d
+
+    sets = [experts() for _ in range(copies)]
+    out = {}
+    for T in (1, 16, 256):
+        routes = []
+        touched = 0
+        for r in range(copies):
+            logits = torch.randn((T, E), generator=g)
+            w, ids = torch.topk(logits, top_k, dim=1)
+            routes.append((ids.to(torch.int32).to(dev), torch.softmax(w, dim=1).to(dev)))
+            touched += len(torch.unique(ids))
+        x = torch.randn((T, H), generator=g).half().to(dev)
+        y = torch.empty((T, H), dtype=torch.float16, device=dev)
+        us = _graph_us(torch, lambda i: ops.moe_forward(x, routes[i % copies][0], routes[i % copies][1],
+                                                       sets[i % copies], 1, out=y), copies * 4)
+        nbytes = touched / copies * 1786368 + T * (8192 + 64)
+        out[f"T{T}"] = {"us": round(us, 1), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "experts_touched": round(touched / copies, 1),
+                        "TFLOPS": round(T * 75497472 / (us * 1e-6) / 1e12, 2)}
+        print(f"[bench] moe T={T}: {us:.1f} us, {out[f'T{T}']['GB/s']} GB/s", file=sys.stderr, flush=True)
+    return out
+
+
+def bench_kv(torch, ops, dev) -> dict:
+    """quantized-KV decode attention, 40 query / 8 KV heads, head_dim 128, batch 16, context 4k
+    and 32k, 16-token pages in a random page order, 8- and 4-bit codes with per-(page, head) fp16 scales.  Rotating
+    cache copies keep >= 512 MB in play at 4k.  Bytes = codes + scales + page table + q/out."""
+    B, Hq, Hkv, D = 16, 40, 8, 128
+    g = torch.Generator(device="cpu").manual_seed(13)
+    out = {}
+    for L in (4096, 32768):
+        for bits in (8, 4):
+            npg = L // 16
+            P = B * npg
+            row = D if bits == 8 else D // 2
+            copies = 4 if L == 4096 else 1
+            sets = []
+            for _ in range(copies):
+                kc = torch.randint(-128, 128, (P, Hkv, 16, row), dtype=torch.int8, device=dev)
+                vc = torch.randint(-128, 128, (P, Hkv, 16, row), dtype=torch.int8, device=dev)
+                ks = (torch.rand((P, Hkv), device=dev) * 0.02 + 0.01).half()
+                vs = (torch.rand((P, Hkv), device=dev) * 0.02 + 0.01).half()
+                table = torch.randperm(P, generator=g).to(torch.int32).view(B, npg).to(dev)
+                sets.append((kc, vc, ks, vs, table))
+            q = torch.randn((B, Hq, D), generator=g).half().to(dev)
+            lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+            o = torch.empty((B, Hq, D), dtype=torch.float16, device=dev)
+            us = _graph_us(torch, lambda i: ops.kv_decode_attention(q, *sets[i % copies][:4], sets[i % copies][4],
+                                                                    lens, bits, out=o), copies * 8)
+            nbytes = 2 * B * Hkv * L * row + 2 * 2 * P * Hkv + 4 * B * npg + 2 * 2 * B * Hq * D
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out[f"L{L // 1024}k_{bits}bit"] = {"us": round(us, 1), "GB/s": round(gbs, 1),
+                                               "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+            print(f"[bench] kv L={L} bits={bits}: {us:.1f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+            del sets
+    torch.cuda.empty_cache()
+    return out
 
 
 def _under_profiler() -> bool:
@@ -215,6 +331,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--extra-rows", default="4,16", help="also report these M (comma list, '' for none)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the prefill / MoE / KV-attention lines")
     ap.add_argument("--probe", choices=["gate_up", "copy"], help=argparse.SUPPRESS)
     ap.add_argument("--probe-launches", type=int, default=20, help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -263,7 +380,7 @@ def main() -> int:
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     all_ms = sum(main_r["per_layer"].values())
     line = {
-        "metric": "EXL3 decode-GEMV HBM GB/s at M=1 (27B layer set, K=3 MCG)",
+        "metric": "EXL3 GEMV HBM GB/s (% peak) at M=1; decode-GEMM TFLOPS at M=2048",
         "value": round(main_r["gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -290,6 +407,13 @@ def main() -> int:
         "other_rows": {str(M): {"GB/s": round(r["gbs"], 1), "us_per_step": round(r["ms_per_step"] * 1e3, 2)}
                        for M, r in results.items() if M != args.rows},
     }
+    if not args.no_secondary:
+        del sets
+        torch.cuda.empty_cache()
+        line["prefill_decode_gemm"] = bench_prefill(torch, ops, dev)
+        line["decode_gemm_tflops_m2048"] = line["prefill_decode_gemm"]["K3_mcg_M2048"]["TFLOPS"]
+        line["moe_layer"] = bench_moe(torch, ops, dev)
+        line["kv_decode_attention"] = bench_kv(torch, ops, dev)
     if traffic is not None:
         line["roofline"]["traffic_detail"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                               for k, v in traffic.items()}
