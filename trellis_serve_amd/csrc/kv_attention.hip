@@ -18,9 +18,11 @@
 //   O^T += V^T P^T  8 x MFMA 16x16x16 f16.  A = V^T (lane: dim 8(l%16) + db for block db, keys 4(l/16)..+3): the
 //                   lane loads 8 bytes of each of its 4 keys and transposes the 4 x 4 byte blocks with v_perm.
 //                   C lane: dims 32(l/16) .. +31 of query l%16 over the 8 blocks.
-// Codes become fp16 exactly: code + bias (one xor) as the low byte under 0x64 is the fp16 1024 + code + bias, and one
-// packed fp16 subtract of 1024 + bias leaves the code (integers of magnitude <= 128 are exact in fp16).  The four
-// waves merge their (m, l, O) in LDS; the workgroup writes its chunk's partial state and kv_merge_kernel combines the
+// Codes become fp16 without conversions: code + bias (bias 128 / 8, one xor) as the low byte (nibble) under 0x64 is
+// the fp16 1024 + bias + code.  V: one packed fp16 subtract of 1024 + bias leaves the code exactly (integers of
+// magnitude <= 128 are exact in fp16) before it is accumulated.  K: the MFMA takes the biased codes and the page's
+// logits subtract (1024 + bias) * sum(q) -- a per-page correction, never accumulated across pages.  The four waves
+// merge their (m, l, O) in LDS; the workgroup writes its chunk's partial state and kv_merge_kernel combines the
 // chunks by log-sum-exp, in chunk order (deterministic).  Logits are kept in the base-2 domain (scale * log2 e).
 #include <math.h>
 #include <stdint.h>
