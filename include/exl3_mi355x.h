@@ -35,6 +35,12 @@ enum {
 
 #define EXL3_MAX_SHARDS 4
 
+/* The first EXL3_WORKSPACE_COUNTER_BYTES of every exl3_linear / exl3_gemm_rotated / exl3_moe_forward workspace hold
+ * the split counters (one int per output column block).  They must be zero before the first call on a workspace;
+ * every call leaves them zero again, so calls of any shapes may share one workspace (ordered on one stream).  The
+ * region sits at a fixed place so that no call reads another call's partials as counters. */
+#define EXL3_WORKSPACE_COUNTER_BYTES (256u * 1024u)
+
 /* One matrix of a fused group (q/k/v, gate/up): all shards read the same input x and write adjacent column spans
  * of y in order.  Replaces the per-shard tensors of exl3_linear_marlin_multi_out (cuda/csrc/exl3_marlin.cu:507-527)
  * and the shard map of the Marlin template (exl3_marlin_template.h:298-302, 605-610). */
@@ -69,9 +75,9 @@ int exl3_had_out_into(const void* y, int rows, int n, const void* svh, void* out
 
 /* ---- fused decode-GEMV / GEMM (subsystems 2, 3) --------------------------------------------------------------- */
 /* Workspace bytes exl3_linear / exl3_gemm_rotated need for `rows` rows of a group with input width k and
- * `n_total` output columns; 0 means none.  Deterministic in its arguments.  The workspace holds per-column-block
- * split counters and fp32 split partials: it must be zero-filled before its first use (every call leaves the
- * counters at zero again), and calls that share a workspace must be ordered on one stream. */
+ * `n_total` output columns (n_total / 128 at most EXL3_WORKSPACE_COUNTER_BYTES / 4); 0 means none.  Deterministic in its
+ * arguments.  The workspace holds the split counters (EXL3_WORKSPACE_COUNTER_BYTES, zero before the first use) and
+ * fp32 split partials; calls that share a workspace must be ordered on one stream. */
 size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K);
 
 /* y[rows, sum n_s] = concat_s( Had128(Had128(x * suh_s) @ W_s) * svh_s ) with fp32 accumulation; fp16 output of
@@ -112,8 +118,9 @@ typedef struct exl3_moe_weights {
   const void* down_svh;     /* fp16 [E][H] */
 } exl3_moe_weights;
 
-/* Workspace bytes of exl3_moe_forward (routing lists, fp16 g|u and down rows, split counters, fp32 partials).  Must
- * be zero-filled before its first use (the split counters return to zero after every call). */
+/* Workspace bytes of exl3_moe_forward (split counters, routing lists, fp16 g|u and down rows, fp32 partials).  The
+ * counter region (EXL3_WORKSPACE_COUNTER_BYTES, holding num_experts * (2 inter + hidden) / 128 counters) must be
+ * zero before the first use; every call leaves it zero. */
 size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K);
 /* y[t] = sum_j w[t, j] * down_e(fp16(silu(gate_e(x[t])) * up_e(x[t]))), e = topk_ids[t, j]; every linear is an EXL3
  * linear with its own suh / svh; fp32 combine in slot order; ids outside [0, E) are skipped.  x fp16|bf16 [T, H],

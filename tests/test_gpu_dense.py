@@ -196,3 +196,19 @@ def test_invalid_shapes_raise():
         ops.linear(torch.zeros((1, 64), dtype=torch.float16, device="cuda"), [t],
                    [torch.ones(128, dtype=torch.float16, device="cuda")],
                    [torch.ones(128, dtype=torch.float16, device="cuda")], 1)
+
+
+def test_workspace_shared_by_calls_of_different_shapes(coracle):
+    """One workspace serves calls of any shapes: a call with many k-splits leaves fp32 partials behind its counters;
+    a later call with more output column blocks must still see zero counters (they sit in a fixed region)."""
+    ops = _ops()
+    ops._workspace.clear()
+    rng = np.random.default_rng(10)
+    K, cb = 3, 1
+    for k, n, M in ((8192, 128, 16), (256, 12800, 1), (1024, 4096, 3), (8192, 128, 16)):
+        tr, suh, svh = _trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)
+        x = rng.standard_normal((M, k)).astype(np.float16)
+        y = ops.linear(_dev(x), [_dev(tr)], [_dev(suh)], [_dev(svh)], cb).cpu().numpy()
+        ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
+        nrel, mrel = _errs(y, ref)
+        assert nrel <= TOL and mrel <= TOL, (k, n, M, nrel, mrel)

@@ -73,3 +73,20 @@ def test_moe_bf16_and_determinism():
     for _ in range(5):
         assert torch.equal(ops.moe_forward(x.half(), ids, w, st, 1), first)
         assert torch.equal(ops.moe_forward(x, ids, w, st, 1), yb)
+
+
+def test_moe_workspace_shared_by_calls_of_different_shapes():
+    """A call with many slots, then calls with fewer slots and another layer shape, on one workspace: the split
+    counters sit in a fixed region, so no call reads an earlier call's rows or partials as counters."""
+    from trellis_serve_amd import ops
+    ops._moe_ws.clear()
+    rng = np.random.default_rng(11)
+    for E, H, I, T, top_k in ((16, 256, 256, 64, 4), (16, 256, 256, 1, 4), (8, 512, 128, 3, 2), (16, 256, 256, 9, 4)):
+        ex = _experts(rng, E, H, I, 3)
+        x = (rng.standard_normal((T, H)) * 0.5).astype(np.float16)
+        ids = np.stack([rng.permutation(E)[:top_k] for _ in range(T)]).astype(np.int32)
+        w = rng.random((T, top_k)).astype(np.float32)
+        y = ops.moe_forward(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(),
+                            _stack(ex), 1).cpu().numpy()
+        nrel, mrel = _errs(y, orc.moe_forward(x, ids, w, ex, 3, 1))
+        assert nrel <= 2e-3 and mrel <= 2e-3, (E, H, I, T, nrel, mrel)

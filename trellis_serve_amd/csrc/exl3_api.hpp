@@ -28,6 +28,10 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 #define EXL3_CHECK_LAUNCH() EXL3_CHECK_HIP(hipGetLastError())
 
+// split counters at the start of a linear / MoE workspace (fixed place and size, zero between calls)
+constexpr size_t kCounterBytes = EXL3_WORKSPACE_COUNTER_BYTES;
+constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
+
 inline bool valid_bits(int K) { return K == 2 || K == 3 || K == 4 || K == 5 || K == 6 || K == 8; }
 inline bool valid_cb(int cb) { return cb >= 0 && cb <= 2; }
 

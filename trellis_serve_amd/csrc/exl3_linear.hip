@@ -315,8 +315,12 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K) {
   return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(M, nt, K)};
 }
 
-// workspace layout: [counters: one int per 128-column block, zero between calls][pad to 256 B][fp32 partials]
-static size_t counters_bytes(int n_total) { return ((size_t)(n_total / 128) * sizeof(int) + 255) & ~(size_t)255; }
+// workspace layout: [counter region: one int per 128-column block, zero between calls][fp32 partials]; the region
+// has a fixed size so that a later call of another shape never takes an earlier call's partials for counters
+static size_t counters_bytes(int n_total) {
+  (void)n_total;
+  return kCounterBytes;
+}
 
 #define EXL3_DISPATCH_K_CB(K_, CB_, ...)                                  \
   [&]() -> bool {                                                         \
@@ -341,6 +345,7 @@ static int build_shards(const exl3_shard* shards, int nshards, int k, int K, Sha
     const exl3_shard& sh = shards[s];
     EXL3_CHECK_ARG(sh.trellis && sh.suh && sh.svh, "shard %d: null tensor pointer", s);
     EXL3_CHECK_ARG(sh.n > 0 && sh.n % 128 == 0, "shard %d: n = %d is not a positive multiple of 128", s, sh.n);
+    EXL3_CHECK_ARG(blk + sh.n / 128 <= kMaxCounters, "group of more than %d output columns", kMaxCounters * 128);
     EXL3_CHECK_ARG((int64_t)k * sh.n * K / 8 <= INT32_MAX, "shard %d: trellis of %lld bytes exceeds the 2 GiB buffer range",
                    s, (long long)((int64_t)k * sh.n * K / 8));
     sa->trellis[s] = static_cast<const uint32_t*>(sh.trellis);
@@ -445,7 +450,7 @@ extern "C" int exl3_had_out_into(const void* y, int rows, int n, const void* svh
 
 extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K) {
   (void)K;
-  if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128) return 0;
+  if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128 || n_total / 128 > kMaxCounters) return 0;
   // launches take 16 rows at a time, then the remainder: the workspace must hold either plan's partials
   size_t need = 0;
   for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
@@ -480,6 +485,7 @@ extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* tr
   EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0 && n > 0 && n % 128 == 0,
                  "exl3_gemm_rotated: rows = %d, k = %d, n = %d", rows, k, n);
   EXL3_CHECK_ARG((int64_t)k * n * K / 8 <= INT32_MAX, "exl3_gemm_rotated: trellis exceeds the 2 GiB buffer range");
+  EXL3_CHECK_ARG(n / 128 <= kMaxCounters, "exl3_gemm_rotated: n = %d exceeds %d columns", n, kMaxCounters * 128);
   if (rows == 0) return EXL3_OK;
   const size_t need = exl3_linear_workspace_bytes(rows, k, n, K);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_gemm_rotated: workspace %zu bytes, need %zu",

@@ -268,15 +268,16 @@ static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I) {
   const int slots = tokens * top_k;
   p.splits_gu = moe_splits(slots, E, 2 * I / 128, H);
   p.splits_dn = moe_splits(slots, E, H / 128, I);
-  size_t o = 0;
+  // the split counters first, in the fixed counter region (zero between calls whatever the shapes)
+  p.off_cnt_gu = 0;
+  p.off_cnt_dn = (size_t)E * (2 * I / 128) * 4;
+  size_t o = kCounterBytes;
   p.off_counts = o; o = align256(o + (size_t)E * 4);
   p.off_nactive = o; o = align256(o + 4);
   p.off_active = o; o = align256(o + (size_t)E * 4);
   p.off_lists = o; o = align256(o + (size_t)E * slots * 4);
   p.off_gu = o; o = align256(o + (size_t)slots * 2 * I * 2);
   p.off_dn = o; o = align256(o + (size_t)slots * H * 2);
-  p.off_cnt_gu = o; o = align256(o + (size_t)E * (2 * I / 128) * 4);
-  p.off_cnt_dn = o; o = align256(o + (size_t)E * (H / 128) * 4);
   p.off_partial = o;
   o = align256(o + std::max((size_t)p.splits_gu * slots * 2 * I, (size_t)p.splits_dn * slots * H) * 4);
   p.total = o;
@@ -304,6 +305,7 @@ using namespace exl3;
 extern "C" size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K) {
   (void)K;
   if (tokens <= 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || inter <= 0) return 0;
+  if ((int64_t)num_experts * (2 * inter + hidden) / 128 > kMaxCounters) return 0;
   return moe_plan(tokens, top_k, num_experts, hidden, inter).total;
 }
 
@@ -321,6 +323,9 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
                      w->up_svh && w->down_suh && w->down_svh,
                  "exl3_moe_forward: null expert tensor");
   EXL3_CHECK_ARG((int64_t)hidden * inter * K / 8 <= INT32_MAX, "exl3_moe_forward: expert matrix too large");
+  EXL3_CHECK_ARG((int64_t)num_experts * (2 * inter + hidden) / 128 <= kMaxCounters,
+                 "exl3_moe_forward: %d experts x (2 x %d + %d) / 128 split counters exceed %d", num_experts, inter,
+                 hidden, kMaxCounters);
   if (tokens == 0) return EXL3_OK;
   const int slots = tokens * top_k;
   EXL3_CHECK_ARG((int64_t)slots * std::max(2 * inter, hidden) <= INT32_MAX / 4, "exl3_moe_forward: too many slots");
