@@ -94,11 +94,15 @@ int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int 
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- prefill decode-GEMM (subsystem 3) ------------------------------------------------------------------------ */
-/* Workspace bytes of exl3_linear_prefill: the per-shard rotated activations (fp16 [nshards][rows][k]). */
-size_t exl3_prefill_workspace_bytes(int rows, int k, int nshards);
+/* Workspace bytes of exl3_linear_prefill for `rows` rows of a group with input width k, n_total output columns and
+ * nshards shards: EXL3_WORKSPACE_COUNTER_BYTES of split counters (zero before the first use; every call leaves them
+ * zero), the per-shard rotated activations (fp16 [nshards][rows][k]), then fp32 partials of the k-split tail tiles.
+ * Depends on the current device's CU count. */
+size_t exl3_prefill_workspace_bytes(int rows, int k, int n_total, int nshards);
 /* Same contract as exl3_linear for many rows: the input rotation of every shard goes to the workspace, then one
  * fused decode-GEMM launch (weights decoded into LDS, fp16 MFMA, fp32 accumulation, output rotation in the epilogue)
- * writes y.  Replaces the reference's prefill branch -- rotation, ExLlamaV3 reconstruct, cuBLAS, rotation
+ * writes y.  Tiles that do not fill a whole round of the machine are split along k and summed in a fixed order, so
+ * results do not depend on scheduling.  Replaces the reference's prefill branch -- rotation, ExLlamaV3 reconstruct, cuBLAS, rotation
  * (cuda/src/sglang_exl3/runtime/ops.py:36-59, 87-95). */
 int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards, int K,
                         int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);

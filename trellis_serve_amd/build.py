@@ -56,6 +56,12 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
                        capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    # a kernel template whose host stub the compiler silently dropped links fine but cannot be loaded: fail here
+    nm = subprocess.run(["nm", "-u", tmp], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in nm.stdout.splitlines() if "__device_stub__" in ln]
+    if missing:
+        os.remove(tmp)
+        raise RuntimeError(f"kernel host stubs missing from the link: {missing[:4]}")
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")

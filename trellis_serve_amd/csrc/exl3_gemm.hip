@@ -5,24 +5,35 @@
 // (exl3_marlin_template.h).  Here the weights are decoded into LDS inside the GEMM and never reach HBM.
 //
 // Operands
-//   A: xh in "fragment order": the rotated activations with k permuted inside every 32-wide block so that the 8
-//      halves one MFMA lane needs are contiguous: xh_f[m][32b + 8q + 4tr + e] = xh[m][32b + 16tr + r(q, e)],
-//      r(q, e) = 2q + (e & 1) + 8(e >> 1) (written by had_in_frag_kernel).
+//   A: xh in "fragment order", k-step major: the rotated activations with k permuted inside every 32-wide block so
+//      that the 8 halves one MFMA lane needs are contiguous, and the blocks of one k-step stored together:
+//      xh_f[b][m][8q + 4tr + e] = xh[m][32b + 16tr + r(q, e)], r(q, e) = 2q + (e & 1) + 8(e >> 1) (written by
+//      had_in_frag_kernel).  One k-step of 256 rows is one contiguous 16 KB run: the GEMM's loads use whole lines.
 //   B: the trellis.  A k-step covers 32 rows = 2 tile rows.  The lane-geometry decode of exl3_device.hpp gives lane
 //      (c, j) of a tile the 4 weights of column c at rows r(j, 0..3); tile row tr of the k-step supplies halves
 //      4tr..4tr+3 of the lane's 8-half B fragment.  A and B then agree on the k order of every MFMA.
 //
 // Tiling: workgroup 256 rows x 128 columns (one output rotation block), 4 waves as 2 x 2, wave tile 128 x 64
-// (8 x 4 MFMA 16x16x32 tiles, 128 fp32 accumulators per lane).  Grid: x = column blocks (fastest: consecutive
-// workgroups share the A rows in L2), y = row blocks.
+// (8 x 4 MFMA 16x16x32 tiles, 128 fp32 accumulators per lane).  Two workgroups fit a CU (LDS and VGPRs), so
+// 2 x CUs tiles run at once.
 //
-// Pipeline: kStages-deep LDS ring of raw k-step inputs, filled by direct-to-LDS 16-byte buffer loads (no VGPR
-// staging): per k-step each wave issues 4 A pieces (one m-block of 64 lanes x 16 B each: a lane's 16 bytes land
-// exactly where its MFMA A fragment lives) and 1 piece of trellis bits (its 4 tiles of the k-step).  The compiler
-// does not order LDS-DMA writes before LDS reads, so the waits are explicit: vmcnt(5 (kStages - 2)) leaves the
-// younger stages in flight, and a barrier covers the other waves' pieces.  Each iteration runs the MFMAs of k-step
-// kt next to the decode of k-step kt+1 (16 tiles per workgroup, 4 per wave, into a double-buffered fp16 B fragment
-// area), so VALU decode work overlaps matrix work.
+// Work decomposition (1-D grid of work items, dispatched in order): tiles are numbered column block fastest, so
+// consecutive workgroups share their A rows in L2.  R x slots tiles (R whole rounds of the machine) are data-parallel
+// items covering all of k; the remaining tail tiles, too few to fill a round, are split along k into S items each
+// (S x tail <= slots) so that no round runs a few tiles on an otherwise idle chip.  The split items are dispatched
+// first: they fill the first round together with the first data-parallel tiles, and their reductions overlap the
+// rest of the launch.  A split item stores its fp32 accumulators as a partial; the last of the S items of a tile to
+// arrive (a per-tile counter in the workspace's counter region) sums the S partials in split order (deterministic,
+// independent of arrival order), then runs the same epilogue as a data-parallel item and resets the counter.
+//
+// Pipeline: direct-to-LDS 16-byte buffer loads (no VGPR staging) into two 3-slot rings, one for A (per k-step each
+// wave loads 4 pieces, one m-block of 64 lanes x 16 B: a lane's 16 bytes land exactly where its MFMA A fragment lives)
+// and one for the trellis bits (each wave loads its 4 tiles of the k-step).  A bundle of loads holds A of step b and
+// the bits of step b+1 and is issued two steps before its A is used, so every load has two steps of flight while the
+// LDS stays under 80 KB (two workgroups per CU).  The compiler does not order LDS-DMA writes before LDS reads, so the
+// waits are explicit (vmcnt), and one barrier per k-step publishes the other waves' pieces and decoded weights.
+// Each k-step runs its 32 MFMAs next to the decode of the following k-step (16 tiles per workgroup, 4 per wave, into
+// a double-buffered fp16 B fragment area), so VALU decode work overlaps matrix work.
 #include <stdlib.h>
 
 #include <algorithm>
@@ -34,6 +45,7 @@ namespace exl3 {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBM = 256, kBN = 128, kBK = 32;
 constexpr int kGemmThreads = 256;
@@ -52,24 +64,36 @@ struct GemmShards {
 };
 
 
+// The work decomposition of one launch (see the header comment).
+struct GemmPlan {
+  int cb;          // column blocks (tiles per row block)
+  int dp;          // data-parallel tiles 0 .. dp-1 (items tail * splits ..)
+  int tail;        // tail tiles dp .. dp+tail-1, split along k (items 0 .. tail * splits - 1)
+  int splits;      // k-splits of each tail tile
+  int ksteps;      // k / 32
+  float* partial;  // [tail items][4 waves][8][4][64 lanes] float4: a split item's accumulators
+  int* counters;   // [tail tiles], zero between calls
+};
+
 // Workgroup barrier that waits for this wave's LDS accesses only.  __syncthreads() adds a workgroup fence, which
 // makes the compiler wait for every outstanding load (vmcnt(0)) and would drain the direct-to-LDS pipeline; the
 // direct-to-LDS writes are waited for explicitly (waitcnt_vm) before each barrier instead.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// LDS: a 3-slot ring of A stages (16 KB each), a 3-slot ring of trellis-bits stages (4 KB: each wave's 4 tiles),
+// two decoded-B buffers; the epilogue reuses it for the fp16 C tile
 template <int K>
-__host__ __device__ constexpr int gemm_bits_stage() { return 4 * 32 * K; }  // 4 tiles per wave
-constexpr int kBitsRegion = 64 * 16;  // one 16-byte direct-to-LDS load lands at lane * 16: a full wave's span
-
-// one ring stage: A pieces (kAStage) then the 4 waves' trellis bits regions
+__host__ __device__ constexpr int gemm_chunks() { return 4 * 32 * K / 16; }  // 16-byte pieces of a wave's 4 tiles
+// a wave's direct-to-LDS load puts lane l's 16 bytes at l * 16: every wave owns a full 1 KB region (lanes past its
+// pieces re-read its last piece into their own slots)
 template <int K>
-__host__ __device__ constexpr int gemm_ring_stage() { return kAStage + 4 * kBitsRegion; }
-
-template <int K, int STAGES>
+__host__ __device__ constexpr int gemm_bits_stage() { return 4 * 64 * 16; }
+constexpr int kARing = 3, kBitsRing = 3;
+template <int K>
 __host__ __device__ constexpr int gemm_lds_bytes() {
-  return STAGES * gemm_ring_stage<K>() + 2 * kBStage > 128 * kCStride * 2
-             ? STAGES * gemm_ring_stage<K>() + 2 * kBStage
-             : 128 * kCStride * 2;
+  return kARing * kAStage + kBitsRing * gemm_bits_stage<K>() + 2 * kBStage > kBM * kCStride * 2
+             ? kARing * kAStage + kBitsRing * gemm_bits_stage<K>() + 2 * kBStage
+             : kBM * kCStride * 2;
 }
 
 // rotated activations in fragment order: xh_f[s*rows + r][k] for shard s (see the header comment)
@@ -102,31 +126,46 @@ __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict
   had128_x4(f0, f1, f2, f3);
   const _Float16 h[4] = {(_Float16)(f0 * kHadScale), (_Float16)(f1 * kHadScale), (_Float16)(f2 * kHadScale),
                          (_Float16)(f3 * kHadScale)};
-  _Float16* dst = reinterpret_cast<_Float16*>(xh) + ((size_t)s * rows + r) * k + b * 128;
+  // k-step major: the 32 halves of row r in k-step kt (one MFMA k-block) at [kt][r][32], so that one k-step of a row
+  // block is one contiguous run and every 16-row A piece of the GEMM reads whole cache lines
+  _Float16* dst = reinterpret_cast<_Float16*>(xh) + (size_t)s * rows * k;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int p = 4 * t + i;                // position in the 128-block
     const int blk32 = p >> 5, p32 = p & 31;  // 32-block and position inside it
     const int tr = p32 >> 4, rr = p32 & 15;
     const int q = (rr & 7) >> 1, e = (rr & 1) | ((rr >> 3) << 1);
-    dst[blk32 * 32 + q * 8 + tr * 4 + e] = h[i];
+    dst[((size_t)(b * 4 + blk32) * rows + r) * 32 + q * 8 + tr * 4 + e] = h[i];
   }
 }
 
-template <int K, int CB, bool Y_BF16, int kStages>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, int M, int k, void* __restrict__ y,
-                                                             int n_total, int rotate_out) {
-  constexpr int BITS = gemm_bits_stage<K>();
-  constexpr int RING = gemm_ring_stage<K>();
-  static_assert(BITS <= kBitsRegion, "a wave's 4 tiles fit its bits region");
-  constexpr int CHUNKS = BITS / 16;  // 16-byte pieces of one wave's 4 tiles
+template <int K, int CB, bool Y_BF16>
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmPlan plan, int M, int k,
+                                                             void* __restrict__ y, int n_total, int rotate_out) {
+  constexpr int CHUNKS = gemm_chunks<K>();
   static_assert(CHUNKS <= 64, "one gather per wave per k-step");
-  constexpr int kLoadsPerStage = 5;  // per wave: 4 A pieces + 1 bits piece
+  constexpr int BSTAGE = gemm_bits_stage<K>();
   extern __shared__ __align__(16) uint8_t lds[];
-  uint8_t* ring = lds;                        // [kStages][A pieces | bits of 4 waves]
-  uint8_t* b_lds = lds + kStages * RING;      // [2][kBStage] decoded B fragments
+  uint8_t* a_ring = lds;                                    // [kARing][kAStage]
+  uint8_t* bits_ring = lds + kARing * kAStage;              // [kBitsRing][4 waves][64 lanes][16 B]
+  uint8_t* b_lds = bits_ring + kBitsRing * BSTAGE;          // [2][kBStage] decoded B fragments
 
-  const int nblk = blockIdx.x, mblk = blockIdx.y;
+  // work item -> tile and k-step range: the split items of the tail tiles come first (dispatched while the machine
+  // fills, their reductions overlap the data-parallel tiles), then the data-parallel tiles
+  const int item = blockIdx.x;
+  const int nsplit = plan.tail * plan.splits;
+  int tile, kt0 = 0, kt1 = plan.ksteps, split = -1, sj = 0;
+  if (item >= nsplit) {
+    tile = item - nsplit;
+  } else {
+    sj = item;
+    const int tt = sj / plan.splits;
+    split = sj - tt * plan.splits;
+    tile = plan.dp + tt;
+    kt0 = (int)((int64_t)plan.ksteps * split / plan.splits);
+    kt1 = (int)((int64_t)plan.ksteps * (split + 1) / plan.splits);
+  }
+  const int nblk = tile % plan.cb, mblk = tile / plan.cb;
   int s = 0;
 #pragma unroll
   for (int i = 1; i < EXL3_MAX_SHARDS; i++)
@@ -141,13 +180,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, int M
   const int wm = w >> 1, wn = w & 1;
   const int c = l & 15, j = l >> 4;
 
-  // B: wave w decodes tile row tr = w >> 1, tile columns 4 (w & 1) .. +3 of every k-step
+  // B: wave w loads and decodes tile row btr = w >> 1, tile columns btc .. btc+3 (btc = 4 (w & 1)) of every k-step
   const int btr = w >> 1, btc = 4 * (w & 1);
   const int tile_bytes = 32 * K;
   const int row_bytes = tn * tile_bytes;
   const __amdgpu_buffer_rsrc_t brsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, (k >> 4) * row_bytes, 0x00020000);
-  // lanes past the wave's 4 tiles re-read its last piece (same bytes, never decoded)
   const int bgoff = (tc0 + btc) * tile_bytes + min(l, CHUNKS - 1) * 16;  // + tile row * row_bytes
   const LaneGeo g = lane_geo<K>(c, j);
 
@@ -158,129 +196,213 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, int M
       __builtin_amdgcn_make_buffer_rsrc((void*)xh, (short)0, M * k * 2, 0x00020000);
   int aoff[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int row = min(row0 + (4 * w + i) * 16 + c, M - 1);
-    aoff[i] = (row * k + j * 8) * 2;
+  for (int q = 0; q < 4; q++) {
+    const int row = min(row0 + (4 * w + q) * 16 + c, M - 1);
+    aoff[q] = (row * 32 + j * 8) * 2;  // + k-step * M * 64 bytes
   }
 
-  // stage `slot` of the ring <- the inputs of k-step kd
-  auto issue = [&](int slot, int kd) {
-    const int kt = kd;
-    uint8_t* st = ring + (slot % kStages) * RING;
+  // Loads come in bundles: bundle b = A of step b + trellis bits of step b+1 (5 loads per wave; past the end, steps
+  // clamp to the last one: in range, never used).  Step i of the item (k-step kt0 + i) reads A slot i % 3, decodes
+  // the bits of step i+1 from bits slot (i+1) % 3, and issues bundle i+2, so every load has two steps of flight.
+  const int nk = kt1 - kt0;  // >= 1
+  // (the k-step argument kt is clamped by the caller: no device-only calls inside these lambdas, whose host-side
+  // instantiation would otherwise suppress the kernel's host stub)
+  auto issue_a = [&](int i, int kt) {
+    uint8_t* st = a_ring + (i % kARing) * kAStage;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void*)(st + (4 * w + i) * 1024),
-                                               16, aoff[i], kt * kBK * 2, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, (__attribute__((address_space(3))) void*)(st + kAStage + w * kBitsRegion),
-                                             16, bgoff, (2 * kt + btr) * row_bytes, 0, 0);
+    for (int q = 0; q < 4; q++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void*)(st + (4 * w + q) * 1024),
+                                               16, aoff[q], kt * M * kBK * 2, 0, 0);
   };
-  auto decode_b = [&](int kt) {
-    const uint32_t* tw = reinterpret_cast<const uint32_t*>(ring + (kt % kStages) * RING + kAStage + w * kBitsRegion);
-    uint8_t* dst = b_lds + (kt & 1) * kBStage;
+  auto issue_bits = [&](int i, int kt) {
+    uint8_t* st = bits_ring + (i % kBitsRing) * BSTAGE + w * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, (__attribute__((address_space(3))) void*)st, 16, bgoff,
+                                             (2 * kt + btr) * row_bytes, 0, 0);
+  };
+  // this wave's trellis words of step i (bits slot i % 3)
+  auto read_bits = [&](int i, uint32_t (&bw)[4][2]) {
+    const uint32_t* tw = reinterpret_cast<const uint32_t*>(bits_ring + (i % kBitsRing) * BSTAGE + w * 1024);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      const half4_t v = decode_group<K, CB>(tw[t * 8 * K + g.dw0], tw[t * 8 * K + g.dw1], g);
-      // n-block btc + t, lane (c, j), halves 4 btr .. +3
+      bw[t][0] = tw[t * 8 * K + g.dw0];
+      bw[t][1] = tw[t * 8 * K + g.dw1];
+    }
+  };
+  // decoded weights of this wave's 4 tiles into decoded-B buffer i & 1: n-block btc + t, lane (c, j), halves
+  // 4 btr .. +3
+  auto write_b = [&](int i, const uint32_t (&bw)[4][2]) {
+    uint8_t* dst = b_lds + (i & 1) * kBStage;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const half4_t v = decode_group<K, CB>(bw[t][0], bw[t][1], g);
       *reinterpret_cast<half4_t*>(dst + (((btc + t) * 64 + l) * 16) + btr * 8) = v;
     }
   };
 
   float4_t acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int mi = 0; mi < 8; mi++)
 #pragma unroll
-    for (int jj = 0; jj < 4; jj++) acc[i][jj] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int jj = 0; jj < 4; jj++) acc[mi][jj] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int ksteps = k / kBK;  // >= 4 (k >= 128)
-#pragma unroll
-  for (int p = 0; p < kStages - 1; p++) issue(p, min(p, ksteps - 1));
-  // stage 0 in: everything but the kStages-2 younger stages
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerStage * (kStages - 2)));
-  lds_barrier();
-  decode_b(0);
-  lds_barrier();
-
-  for (int kt = 0; kt < ksteps; kt++) {
-    // keep kStages-1 k-steps in flight; past the end the free slot re-reads the last k-step (in range, never used)
-    issue(kt + kStages - 1, min(kt + kStages - 1, ksteps - 1));
-    // stage kt+1 in: everything but the kStages-2 younger stages
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kLoadsPerStage * (kStages - 2)));
+  issue_bits(0, kt0);
+  issue_a(0, kt0);
+  issue_bits(1, kt0 + min(1, nk - 1));
+  issue_a(1, kt0 + min(1, nk - 1));
+  issue_bits(2, kt0 + min(2, nk - 1));
+  {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(10));  // the bits of step 0 in (bundles 0 and 1 may be in flight)
     lds_barrier();
-    const half8_t* af = reinterpret_cast<const half8_t*>(ring + (kt % kStages) * RING) + (wm * 8) * 64 + l;
-    const half8_t* bf = reinterpret_cast<const half8_t*>(b_lds + (kt & 1) * kBStage) + (wn * 4) * 64 + l;
+    uint32_t bw[4][2];
+    read_bits(0, bw);
+    write_b(0, bw);
+  }
+
+  for (int i = 0; i < nk; i++) {
+    // bundle i in (A of step i, bits of step i+1); bundle i+1 may still be in flight.  The barrier makes every wave's
+    // pieces and decoded weights of step i visible and retires every read of step i-1, freeing A slot (i-1) % 3,
+    // bits slot i % 3 and decoded-B buffer (i+1) & 1.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(5));
+    lds_barrier();
+    issue_a(i + 2, kt0 + min(i + 2, nk - 1));
+    issue_bits(i + 3, kt0 + min(i + 3, nk - 1));
+    const half8_t* af = reinterpret_cast<const half8_t*>(a_ring + (i % kARing) * kAStage) + (wm * 8) * 64 + l;
+    const half8_t* bf = reinterpret_cast<const half8_t*>(b_lds + (i & 1) * kBStage) + (wn * 4) * 64 + l;
     half8_t bv[4], av[8];
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) bv[jj] = bf[jj * 64];
 #pragma unroll
-    for (int i = 0; i < 8; i++) av[i] = af[i * 64];
+    for (int mi = 0; mi < 8; mi++) av[mi] = af[mi * 64];
+    uint32_t bw[4][2];
+    read_bits(i + 1, bw);
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int mi = 0; mi < 8; mi++)
 #pragma unroll
       for (int jj = 0; jj < 4; jj++)
-        acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[jj], acc[i][jj], 0, 0, 0);
-    // the next k-step's weights (at the last step: a stale but valid stage into a buffer nobody reads, keeping the
-    // loop body one scheduling region)
-    decode_b(kt + 1);
-    // interleave: the fragment reads first, then one MFMA per two VALU ops of the next k-step's decode
-    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // DS reads of the fragments
+        acc[mi][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mi], bv[jj], acc[mi][jj], 0, 0, 0);
+    // the next step's weights (at the last step: a stale but valid stage into a buffer nobody reads)
+    write_b(i + 1, bw);
+    // interleave: the fragment and trellis-word reads first, then one MFMA per two VALU ops of the decode, then its
+    // LDS writes
+    __builtin_amdgcn_sched_group_barrier(0x100, 20, 0);  // DS reads
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
+    for (int q = 0; q < 32; q++) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
     }
-    lds_barrier();
+    __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);  // DS writes
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the trailing re-reads of every wave before LDS is reused
   __syncthreads();
 
-  // ---- epilogue, two halves of 128 rows: the waves of that half put their fp16 C rows in LDS, then every 32-lane
-  // group rotates whole rows (128 columns), scales by svh and stores
+  // ---- split item: store the partial; the last of the tile's splits to arrive sums them all in split order
+  if (split >= 0) {
+    __shared__ int last_flag;
+    const int j0 = sj - split;  // the tile's first split item
+    float4_t* mine = reinterpret_cast<float4_t*>(plan.partial) + ((size_t)sj * 4 + w) * 32 * 64 + l;
+#pragma unroll
+    for (int mi = 0; mi < 8; mi++)
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        // device-scope coherent 8-byte stores: the partial is read by a workgroup that may sit on another XCD
+        const float4_t v = acc[mi][jj];
+        uint64_t* d = reinterpret_cast<uint64_t*>(mine + (mi * 4 + jj) * 64);
+        __hip_atomic_store(d, __builtin_bit_cast(uint64_t, f32x2{v.x, v.y}), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(d + 1, __builtin_bit_cast(uint64_t, f32x2{v.z, v.w}), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this thread's partial stores are at the coherence point
+    __syncthreads();
+    const int tt = sj / plan.splits;
+    if (tid == 0) {
+      const int prev = __hip_atomic_fetch_add(&plan.counters[tt], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = prev == plan.splits - 1;
+    }
+    __syncthreads();
+    if (!last_flag) return;
+#pragma unroll
+    for (int mi = 0; mi < 8; mi++)
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) acc[mi][jj] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < plan.splits; sp++) {
+      const float4_t* src = reinterpret_cast<const float4_t*>(plan.partial) + ((size_t)(j0 + sp) * 4 + w) * 32 * 64 + l;
+#pragma unroll
+      for (int mi = 0; mi < 8; mi++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const uint64_t* d = reinterpret_cast<const uint64_t*>(src + (mi * 4 + jj) * 64);
+          const f32x2 a = __builtin_bit_cast(f32x2, __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          const f32x2 b =
+              __builtin_bit_cast(f32x2, __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+          acc[mi][jj] += float4_t{a.x, a.y, b.x, b.y};
+        }
+    }
+    if (tid == 0) __hip_atomic_store(&plan.counters[tt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // ---- epilogue: the whole fp16 C tile (256 x 128, rounded once from fp32) goes to LDS, then thread t rotates row t
+  // in registers -- the 128-point butterfly of had128_x4 with the same pairings and order (h = 1, 2, 4, ..., 64;
+  // lower = a + b, upper = a - b, fp32), so results are identical -- scales by svh (fp16 product) and stores it.
+  // Per-row register butterflies have no cross-lane latency: a lane-parallel rotation chains five LDS permutes per
+  // row.
   _Float16* cl = reinterpret_cast<_Float16*>(lds);
-  const int hw = tid >> 5, t = tid & 31;
-  const int col = nblk * 128 + 4 * t;
-  const uint16_t* svh = sa.svh[s] + (col - sa.col0[s]);
 #pragma unroll
-  for (int half = 0; half < 2; half++) {
-    if (wm == half) {
+  for (int mi = 0; mi < 8; mi++)
 #pragma unroll
-      for (int i = 0; i < 8; i++)
+    for (int jj = 0; jj < 4; jj++)
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
+      for (int r = 0; r < 4; r++) {
+        const int m = wm * 128 + mi * 16 + 4 * j + r;
+        const int n = wn * 64 + jj * 16 + c;
+        cl[m * kCStride + n] = (_Float16)acc[mi][jj][r];
+      }
+  __syncthreads();
+  const int m = row0 + tid;
+  if (m < M) {
+    const half8_t* src = reinterpret_cast<const half8_t*>(cl + tid * kCStride);
+    float v[128];
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const int m = i * 16 + 4 * j + r;
-            const int n = wn * 64 + jj * 16 + c;
-            cl[m * kCStride + n] = (_Float16)acc[i][jj][r];
+    for (int q = 0; q < 16; q++) {
+      const half8_t h = src[q];
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[8 * q + e] = (float)h[e];
+    }
+    const int col = nblk * 128;
+    const half8_t* sv8 = reinterpret_cast<const half8_t*>(sa.svh[s] + (col - sa.col0[s]));
+    uint16_t* yr = static_cast<uint16_t*>(y) + (size_t)m * n_total + col;
+    if (rotate_out) {
+#pragma unroll
+      for (int hs = 1; hs < 128; hs <<= 1)
+#pragma unroll
+        for (int p = 0; p < 128; p++)
+          if (!(p & hs)) {
+            const float a = v[p], bb = v[p + hs];
+            v[p] = a + bb;
+            v[p + hs] = a - bb;
           }
     }
-    __syncthreads();
-    for (int ml = hw; ml < 128; ml += 8) {
-      const int m = row0 + half * 128 + ml;
-      _Float16 h[4];
 #pragma unroll
-      for (int i = 0; i < 4; i++) h[i] = cl[ml * kCStride + 4 * t + i];
+    for (int q = 0; q < 16; q++) {
+      half8_t o;
       if (rotate_out) {
-        float f0 = (float)h[0], f1 = (float)h[1], f2 = (float)h[2], f3 = (float)h[3];
-        had128_x4(f0, f1, f2, f3);
-        const half4_t sv = *reinterpret_cast<const half4_t*>(svh);
-        h[0] = (_Float16)(f0 * kHadScale) * sv.x;
-        h[1] = (_Float16)(f1 * kHadScale) * sv.y;
-        h[2] = (_Float16)(f2 * kHadScale) * sv.z;
-        h[3] = (_Float16)(f3 * kHadScale) * sv.w;
+        const half8_t sv = sv8[q];
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (_Float16)(v[8 * q + e] * kHadScale) * sv[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = (_Float16)v[8 * q + e];
       }
-      if (m < M) {
-        uint16_t* yr = static_cast<uint16_t*>(y) + (size_t)m * n_total + col;
-        if constexpr (Y_BF16) {
-          uint2_t o;
-          o.x = (uint32_t)f32_to_bf16((float)h[0]) | ((uint32_t)f32_to_bf16((float)h[1]) << 16);
-          o.y = (uint32_t)f32_to_bf16((float)h[2]) | ((uint32_t)f32_to_bf16((float)h[3]) << 16);
-          *reinterpret_cast<uint2_t*>(yr) = o;
-        } else {
-          *reinterpret_cast<half4_t*>(yr) = half4_t{h[0], h[1], h[2], h[3]};
-        }
+      if constexpr (Y_BF16) {
+        u32x4 ob;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          ob[e] = (uint32_t)f32_to_bf16((float)o[2 * e]) | ((uint32_t)f32_to_bf16((float)o[2 * e + 1]) << 16);
+        *reinterpret_cast<u32x4*>(yr + 8 * q) = ob;
+      } else {
+        *reinterpret_cast<half8_t*>(yr + 8 * q) = o;
       }
     }
-    __syncthreads();
   }
 }
 
@@ -298,13 +420,57 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, int M
   case KV * 4 + 1: { constexpr int kK = KV, kCB = 1; __VA_ARGS__; return true; }      \
   case KV * 4 + 2: { constexpr int kK = KV, kCB = 2; __VA_ARGS__; return true; }
 
+
+
+// Concurrent workgroups of the device (2 per CU: LDS and VGPRs), per device, queried once.
+static int gemm_slots() {
+  static int slots[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (slots[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    slots[dev] = 2 * cus;
+  }
+  return slots[dev];
+}
+
+struct GemmLayout {
+  int cb, dp, splits, tail, ksteps;
+  size_t xh_bytes, partial_off, total;
+};
+
+// R whole rounds of data-parallel tiles, then the tail tiles split along k so that their items fill at most one
+// round; a split keeps >= 8 k-steps so its pipeline start-up stays small against its work
+static GemmLayout gemm_layout(int rows, int k, int n_total, int nshards) {
+  GemmLayout L{};
+  L.cb = n_total / 128;
+  L.ksteps = k / kBK;
+  const int tiles = ((rows + kBM - 1) / kBM) * L.cb;
+  const int slots = gemm_slots();
+  L.dp = (tiles / slots) * slots;
+  L.tail = tiles - L.dp;
+  L.splits = 1;
+  if (L.tail > 0) L.splits = std::max(1, std::min(slots / L.tail, L.ksteps / 8));
+  if (L.splits == 1) {  // no split: the tail tiles are data-parallel items too
+    L.dp = tiles;
+    L.tail = 0;
+  }
+  // [counter region (fixed place and size)][rotated activations][partials]
+  L.xh_bytes = ((size_t)nshards * rows * k * 2 + 255) & ~(size_t)255;
+  L.partial_off = kCounterBytes + L.xh_bytes;
+  L.total = L.partial_off + (size_t)L.tail * L.splits * kBM * kBN * sizeof(float);
+  return L;
+}
+
 }  // namespace exl3
 
 using namespace exl3;
 
-extern "C" size_t exl3_prefill_workspace_bytes(int rows, int k, int nshards) {
-  if (rows <= 0 || k <= 0 || k % 128 || nshards < 1 || nshards > EXL3_MAX_SHARDS) return 0;
-  return ((size_t)nshards * rows * k * 2 + 255) & ~(size_t)255;
+extern "C" size_t exl3_prefill_workspace_bytes(int rows, int k, int n_total, int nshards) {
+  if (rows <= 0 || k <= 0 || k % 128 || n_total <= 0 || n_total % 128 || nshards < 1 || nshards > EXL3_MAX_SHARDS)
+    return 0;
+  return gemm_layout(rows, k, n_total, nshards).total;
 }
 
 extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host,
@@ -316,9 +482,6 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   EXL3_CHECK_ARG(nshards >= 1 && nshards <= EXL3_MAX_SHARDS, "exl3_linear_prefill: nshards = %d", nshards);
   if (rows == 0) return EXL3_OK;
   EXL3_CHECK_ARG((int64_t)rows * k * 2 <= INT32_MAX, "exl3_linear_prefill: rows * k too large for one launch");
-  const size_t need = exl3_prefill_workspace_bytes(rows, k, nshards);
-  EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_linear_prefill: workspace %zu bytes, need %zu",
-                 workspace_bytes, need);
   GemmShards sa{};
   int col = 0, blk = 0;
   for (int s = 0; s < nshards; s++) {
@@ -328,7 +491,8 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
     EXL3_CHECK_ARG((int64_t)k * sh.n * K / 8 <= INT32_MAX, "shard %d: trellis exceeds the 2 GiB buffer range", s);
     sa.trellis[s] = static_cast<const uint32_t*>(sh.trellis);
     sa.svh[s] = static_cast<const uint16_t*>(sh.svh);
-    sa.xh[s] = static_cast<const uint16_t*>(workspace) + (size_t)s * rows * k;
+    sa.xh[s] = reinterpret_cast<const uint16_t*>(static_cast<const uint8_t*>(workspace) + kCounterBytes) +
+               (size_t)s * rows * k;
     sa.tn[s] = sh.n / 16;
     sa.col0[s] = col;
     sa.blk0[s] = blk;
@@ -337,35 +501,36 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   }
   sa.blk0[nshards] = blk;
   sa.count = nshards;
+  const GemmLayout L = gemm_layout(rows, k, col, nshards);
+  EXL3_CHECK_ARG(workspace && workspace_bytes >= L.total, "exl3_linear_prefill: workspace %zu bytes, need %zu",
+                 workspace_bytes, L.total);
+  EXL3_CHECK_ARG(L.tail <= kMaxCounters, "exl3_linear_prefill: %d tail tiles exceed the counter region", L.tail);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  GemmPlan plan{L.cb, L.dp, L.tail, L.splits, L.ksteps, reinterpret_cast<float*>(ws + L.partial_off),
+                reinterpret_cast<int*>(ws)};
+  uint16_t* xh = reinterpret_cast<uint16_t*>(ws + kCounterBytes);
   hipStream_t st = as_stream(stream);
   // input rotation of every shard, in fragment order
   for (int s = 0; s < nshards; s++) {
     // one launch per shard keeps the per-shard suh contiguous without a concatenated copy
     if (x_bf16)
       had_in_frag_kernel<true><<<dim3((unsigned)((rows * (k / 128) + 7) / 8)), 256, 0, st>>>(
-          x, rows, k, static_cast<const uint16_t*>(shards_host[s].suh), 1,
-          static_cast<uint16_t*>(workspace) + (size_t)s * rows * k);
+          x, rows, k, static_cast<const uint16_t*>(shards_host[s].suh), 1, xh + (size_t)s * rows * k);
     else
       had_in_frag_kernel<false><<<dim3((unsigned)((rows * (k / 128) + 7) / 8)), 256, 0, st>>>(
-          x, rows, k, static_cast<const uint16_t*>(shards_host[s].suh), 1,
-          static_cast<uint16_t*>(workspace) + (size_t)s * rows * k);
+          x, rows, k, static_cast<const uint16_t*>(shards_host[s].suh), 1, xh + (size_t)s * rows * k);
     EXL3_CHECK_LAUNCH();
   }
-  const dim3 grid(blk, (rows + kBM - 1) / kBM);
-  static const int stages = [] {
-    const char* e = getenv("EXL3_GEMM_STAGES");
-    return e && atoi(e) == 4 ? 4 : 3;
-  }();
+  const dim3 grid((unsigned)(L.dp + L.tail * L.splits));
   bool ok;
-#define EXL3_GEMM_LAUNCH(YB, ST)                                                                              \
-  ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB, ST><<<grid, kGemmThreads,                    \
-                                                                    gemm_lds_bytes<kK, ST>(), st>>>(         \
-                                          sa, rows, k, y, col, 1))
-  if (y_bf16) {
-    if (stages == 3) EXL3_GEMM_LAUNCH(true, 3); else EXL3_GEMM_LAUNCH(true, 4);
-  } else {
-    if (stages == 3) EXL3_GEMM_LAUNCH(false, 3); else EXL3_GEMM_LAUNCH(false, 4);
-  }
+#define EXL3_GEMM_LAUNCH(YB)                                                                                   \
+  ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB><<<grid, kGemmThreads, gemm_lds_bytes<kK>(),   \
+                                                                      st>>>(                                  \
+                                          sa, plan, rows, k, y, col, 1))
+  if (y_bf16)
+    EXL3_GEMM_LAUNCH(true);
+  else
+    EXL3_GEMM_LAUNCH(false);
 #undef EXL3_GEMM_LAUNCH
   if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_linear_prefill: unsupported K/codebook");
   EXL3_CHECK_LAUNCH();

@@ -184,11 +184,12 @@ def linear_prefill(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch
     if out is None:
         out = torch.empty((rows, n_total), dtype=x.dtype, device=x.device)
     lib = _lib.load()
-    need = lib.exl3_prefill_workspace_bytes(rows, k, len(arr))
+    need = lib.exl3_prefill_workspace_bytes(rows, k, n_total, len(arr))
     idx = x.device.index if x.device.index is not None else torch.cuda.current_device()
     ws = _prefill_ws.get(idx)
     if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+        # zero-filled once: its split counters start at zero and every call leaves them there
+        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
         _prefill_ws[idx] = ws
     _lib.check(lib.exl3_linear_prefill(rows2d.data_ptr(), int(x.dtype == torch.bfloat16), rows, k, arr, len(arr), K,
                                        int(codebook), out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(),
