@@ -89,18 +89,17 @@ def test_prefill_split_tail_tiles_match_oracle(coracle):
     """More tiles than one round of the machine holds: the tiles past the last whole round run as k-split items whose
     fp32 partials are summed in split order.  The tail (last row block, last column blocks) and a data-parallel tile
     are checked against the float64 oracle, and repeated calls are bit-identical."""
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    slots = 2 * cus
+    slots = torch.cuda.get_device_properties(0).multi_processor_count  # one 256 x 256 tile per CU at a time
     M, k, K, cb = 768, 1024, 3, 1
-    cbk = (slots + 28 + 2) // 3  # 3 row blocks x cbk column blocks = slots + ~28 tail tiles
-    n = 128 * cbk
+    cbk = (slots + 28 + 2) // 3  # 3 row blocks x cbk 256-column tiles = slots + ~28 tail tiles
+    n = 256 * cbk
     rng = np.random.default_rng(14)
     tr, suh, svh = _case(rng, k, n, K)
     x = (rng.standard_normal((M, k)) * 0.5).astype(np.float16)
     args = ([_dev(tr)], [_dev(suh)], [_dev(svh)], cb)
     y = _ops().linear_prefill(_dev(x), *args)
     tail = 3 * cbk - slots
-    c0 = (cbk - tail) * 128  # first column of the tail tiles in the last row block
+    c0 = (cbk - tail) * 256  # first column of the tail tiles in the last row block
     for rows, cols in ((slice(512, 768), slice(c0, n)), (slice(0, 256), slice(0, 512))):
         t = tr[:, cols.start // 16:cols.stop // 16]
         ref = orc.linear_forward(x[rows], t, suh, svh[cols], K, cb, w_inner=c_reconstruct(coracle, t, K, cb),

@@ -47,31 +47,34 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 256, kBN = 128, kBK = 32;
-constexpr int kGemmThreads = 256;
-constexpr int kAStage = kBM * kBK * 2;   // 16 KB: [16 m-blocks][64 lanes][8 halves]
-constexpr int kBStage = kBN * kBK * 2;   // 8 KB:  [8 n-blocks][64 lanes][8 halves]
-constexpr int kCStride = kBN + 8;        // epilogue fp16 C tile row stride (halves)
+constexpr int kBM = 256, kBN = 256, kBK = 32;
+constexpr int kGemmWaves = 8, kGemmThreads = kGemmWaves * 64;
+constexpr int kAStage = kBM * kBK * 2;            // 16 KB: [16 m-blocks][64 lanes][8 halves]
+constexpr int kBStage = kBN * kBK * 2;            // 16 KB: [16 n-blocks][64 lanes][8 halves]
+constexpr int kBitsStage = kGemmWaves * 64 * 16;  // 8 KB: per wave 64 lanes x 16 B (its 4 tiles of a k-step)
+constexpr int kRing = 3;                          // A and bits ring slots
+constexpr int kCStride = kBN + 8;                 // epilogue fp16 C tile row stride (halves)
+constexpr int kLoadRegion = kRing * (kAStage + kBitsStage) + 2 * kBStage;
+constexpr int kGemmLds = kLoadRegion > kBM * kCStride * 2 ? kLoadRegion : kBM * kCStride * 2;  // 135 KB: 1 per CU
 
 struct GemmShards {
   const uint32_t* trellis[EXL3_MAX_SHARDS];
   const uint16_t* svh[EXL3_MAX_SHARDS];
-  const uint16_t* xh[EXL3_MAX_SHARDS];  // per-shard rotated activations in fragment order [M][k]
-  int tn[EXL3_MAX_SHARDS];
-  int col0[EXL3_MAX_SHARDS];
-  int blk0[EXL3_MAX_SHARDS + 1];
+  const uint16_t* xh[EXL3_MAX_SHARDS];  // per-shard rotated activations, fragment order, k-step major
+  int tn[EXL3_MAX_SHARDS];              // tile columns of the shard
+  int col0[EXL3_MAX_SHARDS];            // first output column of the shard
+  int ct0[EXL3_MAX_SHARDS + 1];         // first 256-column tile of the shard (cumulative); ct0[count] = total
   int count;
 };
 
-
 // The work decomposition of one launch (see the header comment).
 struct GemmPlan {
-  int cb;          // column blocks (tiles per row block)
+  int nct;         // 256-column tiles per row block
   int dp;          // data-parallel tiles 0 .. dp-1 (items tail * splits ..)
   int tail;        // tail tiles dp .. dp+tail-1, split along k (items 0 .. tail * splits - 1)
   int splits;      // k-splits of each tail tile
   int ksteps;      // k / 32
-  float* partial;  // [tail items][4 waves][8][4][64 lanes] float4: a split item's accumulators
+  float* partial;  // [tail items][8 waves][8][4][64 lanes] float4: a split item's accumulators
   int* counters;   // [tail tiles], zero between calls
 };
 
@@ -80,21 +83,8 @@ struct GemmPlan {
 // direct-to-LDS writes are waited for explicitly (waitcnt_vm) before each barrier instead.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// LDS: a 3-slot ring of A stages (16 KB each), a 3-slot ring of trellis-bits stages (4 KB: each wave's 4 tiles),
-// two decoded-B buffers; the epilogue reuses it for the fp16 C tile
 template <int K>
 __host__ __device__ constexpr int gemm_chunks() { return 4 * 32 * K / 16; }  // 16-byte pieces of a wave's 4 tiles
-// a wave's direct-to-LDS load puts lane l's 16 bytes at l * 16: every wave owns a full 1 KB region (lanes past its
-// pieces re-read its last piece into their own slots)
-template <int K>
-__host__ __device__ constexpr int gemm_bits_stage() { return 4 * 64 * 16; }
-constexpr int kARing = 3, kBitsRing = 3;
-template <int K>
-__host__ __device__ constexpr int gemm_lds_bytes() {
-  return kARing * kAStage + kBitsRing * gemm_bits_stage<K>() + 2 * kBStage > kBM * kCStride * 2
-             ? kARing * kAStage + kBitsRing * gemm_bits_stage<K>() + 2 * kBStage
-             : kBM * kCStride * 2;
-}
 
 // rotated activations in fragment order: xh_f[s*rows + r][k] for shard s (see the header comment)
 template <bool X_BF16>
@@ -144,11 +134,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
                                                              void* __restrict__ y, int n_total, int rotate_out) {
   constexpr int CHUNKS = gemm_chunks<K>();
   static_assert(CHUNKS <= 64, "one gather per wave per k-step");
-  constexpr int BSTAGE = gemm_bits_stage<K>();
   extern __shared__ __align__(16) uint8_t lds[];
-  uint8_t* a_ring = lds;                                    // [kARing][kAStage]
-  uint8_t* bits_ring = lds + kARing * kAStage;              // [kBitsRing][4 waves][64 lanes][16 B]
-  uint8_t* b_lds = bits_ring + kBitsRing * BSTAGE;          // [2][kBStage] decoded B fragments
+  uint8_t* a_ring = lds;                             // [kRing][kAStage]
+  uint8_t* bits_ring = lds + kRing * kAStage;        // [kRing][8 waves][64 lanes][16 B]
+  uint8_t* b_lds = bits_ring + kRing * kBitsStage;   // [2][kBStage] decoded B fragments
 
   // work item -> tile and k-step range: the split items of the tail tiles come first (dispatched while the machine
   // fills, their reductions overlap the data-parallel tiles), then the data-parallel tiles
@@ -165,63 +154,67 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
     kt0 = (int)((int64_t)plan.ksteps * split / plan.splits);
     kt1 = (int)((int64_t)plan.ksteps * (split + 1) / plan.splits);
   }
-  const int nblk = tile % plan.cb, mblk = tile / plan.cb;
+  const int ct = tile % plan.nct, mblk = tile / plan.nct;
   int s = 0;
 #pragma unroll
   for (int i = 1; i < EXL3_MAX_SHARDS; i++)
-    if (i < sa.count && nblk >= sa.blk0[i]) s = i;
+    if (i < sa.count && ct >= sa.ct0[i]) s = i;
   const int tn = sa.tn[s];
-  const int tc0 = (nblk - sa.blk0[s]) * 8;  // first tile column of this block in the shard
+  const int tc0 = (ct - sa.ct0[s]) * 16;  // first tile column of this tile in the shard
+  const int ntc = min(16, tn - tc0);      // tile columns present: 16, or 8 at the end of a shard of odd 128-blocks
+  const int col0 = sa.col0[s] + tc0 * 16;  // first output column
   const int row0 = mblk * kBM;
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = tid & 63;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w >> 2, wn = w & 3;  // wave tile: rows 128 wm .., columns 64 wn ..
   const int c = l & 15, j = l >> 4;
+  const bool mfma_wave = 4 * wn < ntc;  // wave-uniform: its 64 columns exist
 
-  // B: wave w loads and decodes tile row btr = w >> 1, tile columns btc .. btc+3 (btc = 4 (w & 1)) of every k-step
-  const int btr = w >> 1, btc = 4 * (w & 1);
+  // B: wave w loads and decodes tile row btr = w >> 2, tile columns btc .. btc+3 (btc = 4 (w & 3)) of every k-step;
+  // past the end of a half tile it re-reads the tile's first columns (in range, decoded into n-blocks nobody reads)
+  const int btr = w >> 2, btc = 4 * (w & 3);
   const int tile_bytes = 32 * K;
   const int row_bytes = tn * tile_bytes;
   const __amdgpu_buffer_rsrc_t brsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, (k >> 4) * row_bytes, 0x00020000);
-  const int bgoff = (tc0 + btc) * tile_bytes + min(l, CHUNKS - 1) * 16;  // + tile row * row_bytes
+  const int bgoff = (tc0 + (btc < ntc ? btc : 0)) * tile_bytes + min(l, CHUNKS - 1) * 16;  // + tile row * row_bytes
   const LaneGeo g = lane_geo<K>(c, j);
 
-  // A: wave w loads m-blocks 4w .. 4w+3; lane l of a piece = row (l % 16) of the m-block, k-chunk l / 16.  Rows past
+  // A: wave w loads m-blocks 2w, 2w+1; lane l of a piece = row (l % 16) of the m-block, k-chunk l / 16.  Rows past
   // M re-read row M-1 (finite, only feeds discarded C rows).
   const uint16_t* xh = sa.xh[s];
   const __amdgpu_buffer_rsrc_t arsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)xh, (short)0, M * k * 2, 0x00020000);
-  int aoff[4];
+  int aoff[2];
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int row = min(row0 + (4 * w + q) * 16 + c, M - 1);
+  for (int q = 0; q < 2; q++) {
+    const int row = min(row0 + (2 * w + q) * 16 + c, M - 1);
     aoff[q] = (row * 32 + j * 8) * 2;  // + k-step * M * 64 bytes
   }
 
-  // Loads come in bundles: bundle b = A of step b + trellis bits of step b+1 (5 loads per wave; past the end, steps
+  // Loads come in bundles: bundle b = A of step b + trellis bits of step b+1 (3 loads per wave; past the end, steps
   // clamp to the last one: in range, never used).  Step i of the item (k-step kt0 + i) reads A slot i % 3, decodes
   // the bits of step i+1 from bits slot (i+1) % 3, and issues bundle i+2, so every load has two steps of flight.
   const int nk = kt1 - kt0;  // >= 1
   // (the k-step argument kt is clamped by the caller: no device-only calls inside these lambdas, whose host-side
   // instantiation would otherwise suppress the kernel's host stub)
   auto issue_a = [&](int i, int kt) {
-    uint8_t* st = a_ring + (i % kARing) * kAStage;
+    uint8_t* st = a_ring + (i % kRing) * kAStage;
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void*)(st + (4 * w + q) * 1024),
+    for (int q = 0; q < 2; q++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (__attribute__((address_space(3))) void*)(st + (2 * w + q) * 1024),
                                                16, aoff[q], kt * M * kBK * 2, 0, 0);
   };
   auto issue_bits = [&](int i, int kt) {
-    uint8_t* st = bits_ring + (i % kBitsRing) * BSTAGE + w * 1024;
+    uint8_t* st = bits_ring + (i % kRing) * kBitsStage + w * 1024;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, (__attribute__((address_space(3))) void*)st, 16, bgoff,
                                              (2 * kt + btr) * row_bytes, 0, 0);
   };
   // this wave's trellis words of step i (bits slot i % 3)
   auto read_bits = [&](int i, uint32_t (&bw)[4][2]) {
-    const uint32_t* tw = reinterpret_cast<const uint32_t*>(bits_ring + (i % kBitsRing) * BSTAGE + w * 1024);
+    const uint32_t* tw = reinterpret_cast<const uint32_t*>(bits_ring + (i % kRing) * kBitsStage + w * 1024);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
       bw[t][0] = tw[t * 8 * K + g.dw0];
@@ -251,7 +244,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
   issue_a(1, kt0 + min(1, nk - 1));
   issue_bits(2, kt0 + min(2, nk - 1));
   {
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(10));  // the bits of step 0 in (bundles 0 and 1 may be in flight)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(6));  // the bits of step 0 in (bundles 0 and 1 may be in flight)
     lds_barrier();
     uint32_t bw[4][2];
     read_bits(0, bw);
@@ -262,24 +255,26 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
     // bundle i in (A of step i, bits of step i+1); bundle i+1 may still be in flight.  The barrier makes every wave's
     // pieces and decoded weights of step i visible and retires every read of step i-1, freeing A slot (i-1) % 3,
     // bits slot i % 3 and decoded-B buffer (i+1) & 1.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(5));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(3));
     lds_barrier();
     issue_a(i + 2, kt0 + min(i + 2, nk - 1));
     issue_bits(i + 3, kt0 + min(i + 3, nk - 1));
-    const half8_t* af = reinterpret_cast<const half8_t*>(a_ring + (i % kARing) * kAStage) + (wm * 8) * 64 + l;
-    const half8_t* bf = reinterpret_cast<const half8_t*>(b_lds + (i & 1) * kBStage) + (wn * 4) * 64 + l;
-    half8_t bv[4], av[8];
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) bv[jj] = bf[jj * 64];
-#pragma unroll
-    for (int mi = 0; mi < 8; mi++) av[mi] = af[mi * 64];
     uint32_t bw[4][2];
     read_bits(i + 1, bw);
+    if (mfma_wave) {
+      const half8_t* af = reinterpret_cast<const half8_t*>(a_ring + (i % kRing) * kAStage) + (wm * 8) * 64 + l;
+      const half8_t* bf = reinterpret_cast<const half8_t*>(b_lds + (i & 1) * kBStage) + (wn * 4) * 64 + l;
+      half8_t bv[4], av[8];
 #pragma unroll
-    for (int mi = 0; mi < 8; mi++)
+      for (int jj = 0; jj < 4; jj++) bv[jj] = bf[jj * 64];
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++)
-        acc[mi][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mi], bv[jj], acc[mi][jj], 0, 0, 0);
+      for (int mi = 0; mi < 8; mi++) av[mi] = af[mi * 64];
+#pragma unroll
+      for (int mi = 0; mi < 8; mi++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+          acc[mi][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mi], bv[jj], acc[mi][jj], 0, 0, 0);
+    }
     // the next step's weights (at the last step: a stale but valid stage into a buffer nobody reads)
     write_b(i + 1, bw);
     // interleave: the fragment and trellis-word reads first, then one MFMA per two VALU ops of the decode, then its
@@ -299,7 +294,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
   if (split >= 0) {
     __shared__ int last_flag;
     const int j0 = sj - split;  // the tile's first split item
-    float4_t* mine = reinterpret_cast<float4_t*>(plan.partial) + ((size_t)sj * 4 + w) * 32 * 64 + l;
+    float4_t* mine = reinterpret_cast<float4_t*>(plan.partial) + ((size_t)sj * kGemmWaves + w) * 32 * 64 + l;
 #pragma unroll
     for (int mi = 0; mi < 8; mi++)
 #pragma unroll
@@ -326,7 +321,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
 #pragma unroll
       for (int jj = 0; jj < 4; jj++) acc[mi][jj] = float4_t{0.f, 0.f, 0.f, 0.f};
     for (int sp = 0; sp < plan.splits; sp++) {
-      const float4_t* src = reinterpret_cast<const float4_t*>(plan.partial) + ((size_t)(j0 + sp) * 4 + w) * 32 * 64 + l;
+      const float4_t* src =
+          reinterpret_cast<const float4_t*>(plan.partial) + ((size_t)(j0 + sp) * kGemmWaves + w) * 32 * 64 + l;
 #pragma unroll
       for (int mi = 0; mi < 8; mi++)
 #pragma unroll
@@ -341,26 +337,29 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
     if (tid == 0) __hip_atomic_store(&plan.counters[tt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  // ---- epilogue: the whole fp16 C tile (256 x 128, rounded once from fp32) goes to LDS, then thread t rotates row t
-  // in registers -- the 128-point butterfly of had128_x4 with the same pairings and order (h = 1, 2, 4, ..., 64;
-  // lower = a + b, upper = a - b, fp32), so results are identical -- scales by svh (fp16 product) and stores it.
-  // Per-row register butterflies have no cross-lane latency: a lane-parallel rotation chains five LDS permutes per
-  // row.
+  // ---- epilogue: the whole fp16 C tile (256 x 256, rounded once from fp32) goes to LDS, then each thread rotates
+  // one 128-column half-row in registers -- the 128-point butterfly of had128_x4 with the same pairings and order
+  // (h = 1, 2, 4, ..., 64; lower = a + b, upper = a - b, fp32), so results are identical -- scales by svh (fp16
+  // product) and stores it.  Per-row register butterflies have no cross-lane latency: a lane-parallel rotation chains
+  // five LDS permutes per row.
   _Float16* cl = reinterpret_cast<_Float16*>(lds);
+  if (mfma_wave) {
 #pragma unroll
-  for (int mi = 0; mi < 8; mi++)
+    for (int mi = 0; mi < 8; mi++)
 #pragma unroll
-    for (int jj = 0; jj < 4; jj++)
+      for (int jj = 0; jj < 4; jj++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = wm * 128 + mi * 16 + 4 * j + r;
-        const int n = wn * 64 + jj * 16 + c;
-        cl[m * kCStride + n] = (_Float16)acc[mi][jj][r];
-      }
+        for (int r = 0; r < 4; r++) {
+          const int m = wm * 128 + mi * 16 + 4 * j + r;
+          const int n = wn * 64 + jj * 16 + c;
+          cl[m * kCStride + n] = (_Float16)acc[mi][jj][r];
+        }
+  }
   __syncthreads();
-  const int m = row0 + tid;
-  if (m < M) {
-    const half8_t* src = reinterpret_cast<const half8_t*>(cl + tid * kCStride);
+  const int er = tid & (kBM - 1), eh = tid / kBM;  // row and 128-column half of this thread
+  const int m = row0 + er;
+  if (m < M && 8 * eh < ntc) {
+    const half8_t* src = reinterpret_cast<const half8_t*>(cl + er * kCStride + eh * 128);
     float v[128];
 #pragma unroll
     for (int q = 0; q < 16; q++) {
@@ -368,7 +367,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
 #pragma unroll
       for (int e = 0; e < 8; e++) v[8 * q + e] = (float)h[e];
     }
-    const int col = nblk * 128;
+    const int col = col0 + eh * 128;
     const half8_t* sv8 = reinterpret_cast<const half8_t*>(sa.svh[s] + (col - sa.col0[s]));
     uint16_t* yr = static_cast<uint16_t*>(y) + (size_t)m * n_total + col;
     if (rotate_out) {
@@ -422,31 +421,39 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
 
 
 
-// Concurrent workgroups of the device (2 per CU: LDS and VGPRs), per device, queried once.
+// Concurrent workgroups of the device (one per CU: 135 KB of LDS), per device, queried once.
 static int gemm_slots() {
   static int slots[64] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
   if (slots[dev] == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    slots[dev] = 2 * cus;
+    slots[dev] = cus;
   }
   return slots[dev];
 }
 
 struct GemmLayout {
-  int cb, dp, splits, tail, ksteps;
+  int nct, dp, splits, tail, ksteps;
   size_t xh_bytes, partial_off, total;
 };
 
+// 256-column tiles never straddle shards (each shard reads its own rotated activations): a shard of an odd number
+// of 128-column blocks ends in a half tile
+static int gemm_col_tiles(const int* shard_n, int nshards) {  // tiles of 256 columns over all shards
+  int t = 0;
+  for (int s = 0; s < nshards; s++) t += (shard_n[s] / 128 + 1) / 2;
+  return t;
+}
+
 // R whole rounds of data-parallel tiles, then the tail tiles split along k so that their items fill at most one
 // round; a split keeps >= 8 k-steps so its pipeline start-up stays small against its work
-static GemmLayout gemm_layout(int rows, int k, int n_total, int nshards) {
+static GemmLayout gemm_layout(int rows, int k, int nct, int nshards) {
   GemmLayout L{};
-  L.cb = n_total / 128;
+  L.nct = nct;
   L.ksteps = k / kBK;
-  const int tiles = ((rows + kBM - 1) / kBM) * L.cb;
+  const int tiles = ((rows + kBM - 1) / kBM) * nct;
   const int slots = gemm_slots();
   L.dp = (tiles / slots) * slots;
   L.tail = tiles - L.dp;
@@ -470,7 +477,12 @@ using namespace exl3;
 extern "C" size_t exl3_prefill_workspace_bytes(int rows, int k, int n_total, int nshards) {
   if (rows <= 0 || k <= 0 || k % 128 || n_total <= 0 || n_total % 128 || nshards < 1 || nshards > EXL3_MAX_SHARDS)
     return 0;
-  return gemm_layout(rows, k, n_total, nshards).total;
+  // the column-tile count depends on how n_total splits into shards (a shard of an odd number of 128-column blocks
+  // ends in a half tile): take the largest need over every possible count
+  size_t need = 0;
+  for (int nct = (n_total / 128 + 1) / 2; nct <= (n_total / 128 + nshards) / 2; nct++)
+    need = std::max(need, gemm_layout(rows, k, nct, nshards).total);
+  return need;
 }
 
 extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host,
@@ -483,7 +495,8 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   if (rows == 0) return EXL3_OK;
   EXL3_CHECK_ARG((int64_t)rows * k * 2 <= INT32_MAX, "exl3_linear_prefill: rows * k too large for one launch");
   GemmShards sa{};
-  int col = 0, blk = 0;
+  int col = 0, ctl = 0;
+  int shard_n[EXL3_MAX_SHARDS];
   for (int s = 0; s < nshards; s++) {
     const exl3_shard& sh = shards_host[s];
     EXL3_CHECK_ARG(sh.trellis && sh.suh && sh.svh, "shard %d: null tensor pointer", s);
@@ -495,18 +508,19 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
                (size_t)s * rows * k;
     sa.tn[s] = sh.n / 16;
     sa.col0[s] = col;
-    sa.blk0[s] = blk;
+    sa.ct0[s] = ctl;
+    shard_n[s] = sh.n;
     col += sh.n;
-    blk += sh.n / 128;
+    ctl += (sh.n / 128 + 1) / 2;
   }
-  sa.blk0[nshards] = blk;
+  sa.ct0[nshards] = ctl;
   sa.count = nshards;
-  const GemmLayout L = gemm_layout(rows, k, col, nshards);
+  const GemmLayout L = gemm_layout(rows, k, gemm_col_tiles(shard_n, nshards), nshards);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= L.total, "exl3_linear_prefill: workspace %zu bytes, need %zu",
                  workspace_bytes, L.total);
   EXL3_CHECK_ARG(L.tail <= kMaxCounters, "exl3_linear_prefill: %d tail tiles exceed the counter region", L.tail);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  GemmPlan plan{L.cb, L.dp, L.tail, L.splits, L.ksteps, reinterpret_cast<float*>(ws + L.partial_off),
+  GemmPlan plan{L.nct, L.dp, L.tail, L.splits, L.ksteps, reinterpret_cast<float*>(ws + L.partial_off),
                 reinterpret_cast<int*>(ws)};
   uint16_t* xh = reinterpret_cast<uint16_t*>(ws + kCounterBytes);
   hipStream_t st = as_stream(stream);
@@ -524,8 +538,7 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   const dim3 grid((unsigned)(L.dp + L.tail * L.splits));
   bool ok;
 #define EXL3_GEMM_LAUNCH(YB)                                                                                   \
-  ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB><<<grid, kGemmThreads, gemm_lds_bytes<kK>(),   \
-                                                                      st>>>(                                  \
+  ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB><<<grid, kGemmThreads, kGemmLds, st>>>(      \
                                           sa, plan, rows, k, y, col, 1))
   if (y_bf16)
     EXL3_GEMM_LAUNCH(true);
