@@ -11,8 +11,9 @@ before timing starts; R rotating copies of the layer set (>= 512 MB, twice the 2
 Prints one JSON line: metric/value = algorithmic HBM GB/s of the layer set at M = 1 (trellis + sign vectors +
 activations in/out, BASELINE.md C2 = 128,174,080 B per step), plus the roofline of the dominant kernel (the fused
 decode-GEMV), the CPU baseline (the numpy oracle, 1 core, on a bounded sample), the M = 4 / 16 rates, and the other
-configs as reported fields: the prefill decode-GEMM TFLOPS (configs[2], `decode_gemm_tflops_m2048` is the second half
-of the metric), the MoE layer and the quantized-KV decode attention.
+configs as reported fields: the single 4096 x 4096 linear of configs[0] (K = 4, 3INST, M = 1), the prefill decode-GEMM
+TFLOPS (configs[2], `decode_gemm_tflops_m2048` is the second half of the metric), the MoE layer and the
+quantized-KV decode attention.
 """
 from __future__ import annotations
 
@@ -155,6 +156,31 @@ def _graph_us(torch, fn, calls: int, reps: int = 3) -> float:
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (calls * reps)
+
+
+def bench_c1(torch, ops, dev) -> dict:
+    """one 4096 -> 4096 linear, K = 4, 3INST, M = 1 (x fp16 N(0,1)): decode-GEMV with both
+    rotations.  64 rotating copies (537 MB > 2 x the 256 MB MALL) keep the weights cold; the graph replays one call per
+    copy.  Bytes = 8,421,376 per call (trellis + suh + svh + x + y)."""
+    k = n = 4096
+    K, cb, copies = 4, 0, 64
+    g = torch.Generator(device="cpu").manual_seed(14)
+    sets = []
+    for _ in range(copies):
+        tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, generator=g).to(dev)
+        suh = (torch.randint(0, 2, (k,), generator=g) * 2 - 1).half().to(dev)
+        svh = (torch.randint(0, 2, (n,), generator=g) * 2 - 1).half().to(dev)
+        sets.append((tr, suh, svh))
+    x = torch.randn((1, k), generator=g).half().to(dev)
+    y = torch.empty((1, n), dtype=torch.float16, device=dev)
+    us = _graph_us(torch, lambda i: ops.linear(x, [sets[i % copies][0]], [sets[i % copies][1]], [sets[i % copies][2]],
+                                               cb, out=y), copies, reps=4)
+    nbytes = alg_bytes(k, [n], 1, K)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    print(f"[bench] C1 4096x4096 K=4 3inst M=1: {us:.2f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    del sets
+    return {"us": round(us, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+            "bytes": nbytes}
 
 
 def bench_prefill(torch, ops, dev) -> dict:
@@ -410,6 +436,7 @@ def main() -> int:
     if not args.no_secondary:
         del sets
         torch.cuda.empty_cache()
+        line["c1_linear_4096_k4_3inst"] = bench_c1(torch, ops, dev)
         line["prefill_decode_gemm"] = bench_prefill(torch, ops, dev)
         line["decode_gemm_tflops_m2048"] = line["prefill_decode_gemm"]["K3_mcg_M2048"]["TFLOPS"]
         line["moe_layer"] = bench_moe(torch, ops, dev)
