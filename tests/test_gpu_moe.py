@@ -90,3 +90,20 @@ def test_moe_workspace_shared_by_calls_of_different_shapes():
                             _stack(ex), 1).cpu().numpy()
         nrel, mrel = _errs(y, orc.moe_forward(x, ids, w, ex, 3, 1))
         assert nrel <= 2e-3 and mrel <= 2e-3, (E, H, I, T, nrel, mrel)
+
+
+def test_moe_single_token_slot_mode_with_repeated_and_unrouted_ids():
+    """One token runs its top-k slots directly (no routing launch); a repeated expert id and an unrouted slot (-1)
+    in that token must give the exact layer's result (split counters index slots, not experts)."""
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(12)
+    E, H, I, K, top_k = 8, 256, 128, 3, 4
+    ex = _experts(rng, E, H, I, K)
+    x = (rng.standard_normal((1, H)) * 0.5).astype(np.float16)
+    ids = np.array([[3, 3, -1, 6]], dtype=np.int32)
+    w = np.array([[0.4, 0.3, 0.2, 0.1]], dtype=np.float32)
+    for cb in (0, 1):
+        y = ops.moe_forward(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(),
+                            _stack(ex), cb).cpu().numpy()
+        nrel, mrel = _errs(y, orc.moe_forward(x, ids, w, ex, K, cb))
+        assert nrel <= 2e-3 and mrel <= 2e-3, (cb, nrel, mrel)

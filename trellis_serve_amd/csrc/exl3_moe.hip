@@ -8,7 +8,8 @@
 //   y[t] = sum_j w[t, j] * d[slot] in fp32, slot order, one rounding; slots whose expert id is outside [0, E) are
 //          skipped (exl3_marlin_moe.cu:274)
 //
-// Launches (the reference uses five plus an align launch):
+// Launches (the reference uses five plus an align launch; a single token skips the routing launch and runs its top-k
+// slots directly):
 //   moe_route_kernel   one workgroup: per-expert slot counts and lists (LDS atomics), the active experts in
 //                      ascending order.  The order of slots inside an expert's list does not change any result: the
 //                      rows of an MFMA are independent and the combine sums in slot order.
@@ -41,6 +42,8 @@ struct MoeArgs {
   const int* n_active;     // [1]
   const int* active;       // [E]: active experts, ascending
   const int* lists;        // [E][slots]
+  const int* topk_ids;     // [slots]: read directly in slot mode
+  int slot_mode;           // 1: one workgroup row per slot, no routing launch (a single token: its top-k experts)
 };
 
 __global__ __launch_bounds__(1024) void moe_route_kernel(const int* __restrict__ topk_ids, int slots, int E,
@@ -97,10 +100,25 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const 
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
   const int mstride = kMoeNT * 16 + 4;
 
-  if ((int)blockIdx.y >= *a.n_active) return;
-  const int e = a.active[blockIdx.y];
-  const int n_e = a.counts[e];
-  const int* list = a.lists + (size_t)e * a.slots;
+  // expert and its slots: routed mode -- grid row = active expert, its slot list from the routing launch; slot mode
+  // -- grid row = slot, one slot, its expert read from topk_ids (split counters then index slots, so repeated experts
+  // in one token are still right)
+  int e, n_e, ctr_row;
+  const int* list;
+  if (a.slot_mode) {
+    e = a.topk_ids[blockIdx.y];
+    if (e < 0 || e >= a.E) return;
+    n_e = 1;
+    list = nullptr;
+    ctr_row = blockIdx.y;
+  } else {
+    if ((int)blockIdx.y >= *a.n_active) return;
+    e = a.active[blockIdx.y];
+    n_e = a.counts[e];
+    list = a.lists + (size_t)e * a.slots;
+    ctr_row = e;
+  }
+  auto slot_at = [&](int idx) { return a.slot_mode ? (int)blockIdx.y : list[idx]; };
   const int cb = blockIdx.x, sp = blockIdx.z;
   const int k = PHASE ? a.I : a.H;            // input width
   const int n_out = PHASE ? a.H : 2 * a.I;    // output row width (g|u for gate/up)
@@ -128,7 +146,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const 
     for (int u = hw; u < M * NB; u += 2 * kMoeWaves) {
       const int m = u / NB, b = u - m * NB;
       const int kk = (kb0 + b) * 128 + 4 * t;
-      const int slot = list[c0 + m];
+      const int slot = slot_at(c0 + m);
       _Float16 h[4] = {0, 0, 0, 0};
       if (b < nb) {
         float f[4];
@@ -172,14 +190,14 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const 
     for (int r = 0; r < 4; r++) {
       const int m = 4 * j + r;
       if (m < M)
-        __hip_atomic_store(pdst + (size_t)list[c0 + m] * n_out, acc[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pdst + (size_t)slot_at(c0 + m) * n_out, acc[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();  // the next pass restages LDS
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&counters[e * (n_out / 128) + cb], 1, __ATOMIC_RELAXED,
+    const int prev = __hip_atomic_fetch_add(&counters[ctr_row * (n_out / 128) + cb], 1, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev == splits - 1;
   }
@@ -190,7 +208,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const 
   uint16_t* out = PHASE ? dn : gu;
   const int col = cb * 128 + 4 * t;
   for (int m = hw; m < n_e; m += 2 * kMoeWaves) {
-    const int slot = list[m];
+    const int slot = slot_at(m);
     float4_t s4 = {0.f, 0.f, 0.f, 0.f};
     for (int p = 0; p < splits; p++) {
       const float* src = partial + ((size_t)p * a.slots + slot) * n_out + col;
@@ -210,7 +228,7 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const 
     *reinterpret_cast<half4_t*>(out + (size_t)slot * n_out + col) = o;
   }
   if (threadIdx.x == 0)
-    __hip_atomic_store(&counters[e * (n_out / 128) + cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&counters[ctr_row * (n_out / 128) + cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <bool Y_BF16>
@@ -356,6 +374,9 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   a.n_active = nactive;
   a.active = active;
   a.lists = lists;
+  a.topk_ids = static_cast<const int*>(topk_ids);
+  // a single token: its top-k slots run directly (no routing launch); several tokens share experts, so they are routed
+  a.slot_mode = tokens == 1 && slots <= num_experts;
   uint16_t* gu = reinterpret_cast<uint16_t*>(ws + p.off_gu);
   uint16_t* dn = reinterpret_cast<uint16_t*>(ws + p.off_dn);
   int* cnt_gu = reinterpret_cast<int*>(ws + p.off_cnt_gu);
@@ -363,10 +384,12 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   float* partial = reinterpret_cast<float*>(ws + p.off_partial);
   hipStream_t st = as_stream(stream);
 
-  moe_route_kernel<<<1, 1024, 0, st>>>(static_cast<const int*>(topk_ids), slots, num_experts, counts, nactive, active,
-                                       lists);
-  EXL3_CHECK_LAUNCH();
-  const int max_active = std::min(num_experts, slots);
+  if (!a.slot_mode) {
+    moe_route_kernel<<<1, 1024, 0, st>>>(static_cast<const int*>(topk_ids), slots, num_experts, counts, nactive,
+                                         active, lists);
+    EXL3_CHECK_LAUNCH();
+  }
+  const int max_active = a.slot_mode ? slots : std::min(num_experts, slots);
   bool ok = EXL3_MOE_DISPATCH(K, codebook, {
     moe_gemv_kernel<kK, kCB, 0><<<dim3(2 * inter / 128, max_active, p.splits_gu), kMoeThreads, moe_lds_bytes<kK>(),
                                   st>>>(a, x, x_bf16, gu, dn, partial, cnt_gu, p.splits_gu);
