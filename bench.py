@@ -13,7 +13,9 @@ activations in/out, BASELINE.md C2 = 128,174,080 B per step), plus the roofline 
 decode-GEMV), the CPU baseline (the numpy oracle, 1 core, on a bounded sample), the M = 4 / 16 rates, and the other
 configs as reported fields: the single 4096 x 4096 linear of configs[0] (K = 4, 3INST, M = 1), the prefill decode-GEMM
 TFLOPS (configs[2], `decode_gemm_tflops_m2048` is the second half of the metric), the MoE layer and the
-quantized-KV decode attention.
+quantized-KV decode attention.  For scale: the warm (single copy) layer-set rate, the trellis-only
+weight-stream rate, hipBLASLt's fp16 8192^3 GEMM, and the reference's prefill design (W decoded to HBM, then the vendor
+GEMM) rebuilt on this box at configs[2] M = 2048.
 """
 from __future__ import annotations
 
@@ -40,6 +42,8 @@ LAYERS = {  # name: (k, [n per shard])
     "down": (17408, [5120]),
 }
 K_BITS, CODEBOOK = 3, 1  # 3 bpw, MCG
+# trellis bytes of one step (the reference's weight-stream figure, xpu/bench/linear_budget.py:83-88)
+TRELLIS_BYTES_PER_STEP = sum(k * sum(ns) * K_BITS // 8 for k, ns in LAYERS.values())
 
 
 def alg_bytes(k: int, ns: list[int], M: int, K: int) -> int:
@@ -204,6 +208,74 @@ def bench_prefill(torch, ops, dev) -> dict:
         out[f"K{K}_{names[cb]}_M{M}"] = {"us": round(us, 1), "TFLOPS": round(tf, 1),
                                         "pct_mfma_peak": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 2)}
         print(f"[bench] prefill K={K} {names[cb]} M={M}: {us:.1f} us, {tf:.0f} TFLOPS", file=sys.stderr, flush=True)
+    return out
+
+
+def _eager_us(torch, fn, reps: int = 10, warm: int = 3) -> float:
+    """Mean device time of fn() in microseconds over back-to-back eager calls (HIP events on the current stream);
+    for library calls that stay out of graphs."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def bench_vendor(torch, ops, dev) -> dict:
+    """The vendor fp16 GEMM on the same box, for scale: (1) torch.mm (hipBLASLt) on 8192^3 fp16, the practical MFMA
+    ceiling of a plain GEMM; (2) the reference's own prefill design (decode W_inner to HBM, vendor GEMM, output
+    rotation: kernels/reference.py:71-104, runtime/ops.py:36-59) rebuilt from this library's had_in / reconstruct /
+    had_out kernels around torch.mm, at BASELINE configs[2] M = 2048, K = 3 MCG, against the fused decode-GEMM on the
+    same inputs.  Eager launches (each >= tens of us), HIP events."""
+    out = {}
+    g = torch.Generator(device="cpu").manual_seed(21)
+    a = torch.randn((8192, 8192), generator=g).half().to(dev)
+    b = torch.randn((8192, 8192), generator=g).half().to(dev)
+    c = torch.empty((8192, 8192), dtype=torch.float16, device=dev)
+    us = _eager_us(torch, lambda: torch.mm(a, b, out=c))
+    tf = 2.0 * 8192 ** 3 / (us * 1e-6) / 1e12
+    out["hipblaslt_fp16_8192cube"] = {"us": round(us, 1), "TFLOPS": round(tf, 1),
+                                      "pct_mfma_peak": round(100 * tf / MFMA_F16_PEAK_TFLOPS, 2)}
+    print(f"[bench] hipBLASLt fp16 8192^3: {us:.1f} us, {tf:.0f} TFLOPS", file=sys.stderr, flush=True)
+    del a, b, c
+    k, n, M, K, cb = 5120, 17408, 2048, 3, 1
+    tr = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, generator=g).to(dev)
+    suh = (torch.randint(0, 2, (k,), generator=g) * 2 - 1).half().to(dev)
+    svh = (torch.randint(0, 2, (n,), generator=g) * 2 - 1).half().to(dev)
+    x = (torch.randn((M, k), generator=g) * 0.5).half().to(dev)
+    xh = torch.empty((M, k), dtype=torch.float16, device=dev)
+    w = torch.empty((k, n), dtype=torch.float16, device=dev)
+    yr = torch.empty((M, n), dtype=torch.float16, device=dev)
+    y = torch.empty((M, n), dtype=torch.float16, device=dev)
+    yf = torch.empty((M, n), dtype=torch.float16, device=dev)
+
+    def reference_design():
+        ops.had_in_group(x, suh, xh)
+        ops.reconstruct(tr, cb, out=w)
+        torch.mm(xh, w, out=yr)
+        ops.had_out_into(yr, svh, y, 0)
+
+    flops = 2.0 * M * k * n
+    parts = {"reconstruct": lambda: ops.reconstruct(tr, cb, out=w), "gemm": lambda: torch.mm(xh, w, out=yr)}
+    res = {"total": _eager_us(torch, reference_design)}
+    for nm, fn in parts.items():
+        res[nm] = _eager_us(torch, fn)
+    fused = _eager_us(torch, lambda: ops.linear_prefill(x, [tr], [suh], [svh], cb, out=yf))
+    same = (yf.float() - y.float()).norm().item() / max(y.float().norm().item(), 1e-30)
+    out["reference_design_prefill_M2048_K3_mcg"] = {
+        "us": round(res["total"], 1), "TFLOPS": round(flops / (res["total"] * 1e-6) / 1e12, 1),
+        "reconstruct_us": round(res["reconstruct"], 1), "hipblaslt_gemm_us": round(res["gemm"], 1),
+        "hipblaslt_gemm_TFLOPS": round(flops / (res["gemm"] * 1e-6) / 1e12, 1),
+        "fused_decode_gemm_us": round(fused, 1), "fused_TFLOPS": round(flops / (fused * 1e-6) / 1e12, 1),
+        "speedup_fused_vs_reference_design": round(res["total"] / fused, 3),
+        "norm_rel_diff_fused_vs_reference_design": float(f"{same:.3g}")}
+    print(f"[bench] reference design prefill M=2048: {res['total']:.1f} us (reconstruct {res['reconstruct']:.1f}, "
+          f"hipBLASLt {res['gemm']:.1f}); fused {fused:.1f} us; rel diff {same:.2e}", file=sys.stderr, flush=True)
     return out
 
 
@@ -398,6 +470,9 @@ def main() -> int:
               f"per layer us {({k: round(v * 1e3, 1) for k, v in per_layer.items()})}", file=sys.stderr, flush=True)
 
     main_r = results[args.rows]
+    # warm secondary: one copy of the layer set (128 MB, inside the 256 MB MALL) replayed back to back
+    _, warm_ms, _ = time_layer_set(torch, ops, sets[:1], xs_for(args.rows), max(20, args.steps // 4), args.warmup)
+    print(f"[bench] M={args.rows} warm (one copy): {warm_ms * 1e3:.1f} us/step", file=sys.stderr, flush=True)
     # dominant kernel: the gate_up fused linear (one gemv_kernel launch); its per-launch time comes from HIP events
     # around graph replays of that layer alone
     kd, nd = LAYERS[DOMINANT]
@@ -430,6 +505,9 @@ def main() -> int:
         "pct_hbm_peak": round(100 * main_r["gbs"] / HBM_PEAK_GBS, 2),
         "us_per_layer": {k: round(v * 1e3, 2) for k, v in main_r["per_layer"].items()},
         "gemv_kernels_gbs": round(main_r["step_bytes"] / (all_ms * 1e-3) / 1e9, 2),
+        "weight_stream_gbs": round(TRELLIS_BYTES_PER_STEP / (main_r["ms_per_step"] * 1e-3) / 1e9, 2),
+        "warm_single_copy": {"GB/s": round(main_r["step_bytes"] / (warm_ms * 1e-3) / 1e9, 1),
+                             "us_per_step": round(warm_ms * 1e3, 2)},
         "other_rows": {str(M): {"GB/s": round(r["gbs"], 1), "us_per_step": round(r["ms_per_step"] * 1e3, 2)}
                        for M, r in results.items() if M != args.rows},
     }
@@ -439,6 +517,7 @@ def main() -> int:
         line["c1_linear_4096_k4_3inst"] = bench_c1(torch, ops, dev)
         line["prefill_decode_gemm"] = bench_prefill(torch, ops, dev)
         line["decode_gemm_tflops_m2048"] = line["prefill_decode_gemm"]["K3_mcg_M2048"]["TFLOPS"]
+        line["vendor_gemm"] = bench_vendor(torch, ops, dev)
         line["moe_layer"] = bench_moe(torch, ops, dev)
         line["kv_decode_attention"] = bench_kv(torch, ops, dev)
     if traffic is not None:

@@ -107,3 +107,128 @@ def test_moe_single_token_slot_mode_with_repeated_and_unrouted_ids():
                             _stack(ex), cb).cpu().numpy()
         nrel, mrel = _errs(y, orc.moe_forward(x, ids, w, ex, K, cb))
         assert nrel <= 2e-3 and mrel <= 2e-3, (cb, nrel, mrel)
+
+
+def test_moe_combine_edge_rows():
+    """Unrouted slots, a repeated id and a token whose ids are all unrouted (its row is exactly zero, written into an
+    output pre-filled with NaN), top_k = 10 (two chunks of the combine, the second partial): the exact layer's result."""
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(46)
+    E, H, I, K, top_k, T = 16, 256, 128, 3, 10, 6
+    ex = _experts(rng, E, H, I, K)
+    x = (rng.standard_normal((T, H)) * 0.5).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:top_k] for _ in range(T)]).astype(np.int32)
+    ids[0, 1] = -1
+    ids[1, :] = -1
+    ids[2, 9] = ids[2, 0]
+    ids[3, 8] = E
+    w = rng.random((T, top_k)).astype(np.float32)
+    y = torch.full((T, H), float("nan"), dtype=torch.float16, device="cuda")
+    ops.moe_forward(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), _stack(ex),
+                    1, out=y)
+    assert (y[1] == 0).all()
+    nrel, mrel = _errs(y.cpu().numpy(), orc.moe_forward(x, ids, w, ex, K, 1))
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+
+def test_moe_single_token_all_unrouted_is_zero():
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(41)
+    E, H, I, K = 8, 256, 128, 3
+    st = _stack(_experts(rng, E, H, I, K))
+    x = torch.randn((1, H), device="cuda").half()
+    ids = torch.full((1, 4), -1, dtype=torch.int32, device="cuda")
+    ids[0, 2] = E  # out of range too
+    w = torch.rand((1, 4), device="cuda")
+    y = torch.full((1, H), float("nan"), dtype=torch.float16, device="cuda")
+    ops.moe_forward(x, ids, w, st, 1, out=y)
+    assert (y == 0).all()
+
+
+def test_moe_many_slots_use_the_routing_launch():
+    """2080 slots over 8 experts (260 per expert: passes of 64 slots, the last one partial); both ends of the token
+    range against the exact layer, and a repeat is bit-identical."""
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(47)
+    E, H, I, K, top_k, T = 8, 128, 128, 3, 8, 260  # 2080 slots
+    ex = _experts(rng, E, H, I, K)
+    x = (rng.standard_normal((T, H)) * 0.5).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:top_k] for _ in range(T)]).astype(np.int32)
+    ids[5, 3] = -1
+    w = rng.random((T, top_k)).astype(np.float32)
+    args = (torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), _stack(ex), 2)
+    y = ops.moe_forward(*args)
+    for sl in (slice(0, 8), slice(T - 4, T)):
+        nrel, mrel = _errs(y[sl].cpu().numpy(), orc.moe_forward(x[sl], ids[sl], w[sl], ex, K, 2))
+        assert nrel <= 2e-3 and mrel <= 2e-3, (sl, nrel, mrel)
+    assert torch.equal(ops.moe_forward(*args), y)
+
+
+def test_moe_full_shape_batched_tokens_match_single_token(coracle):
+    """BASELINE configs[3] shape (128 experts, top-8, hidden 2048, inter 768, K = 3 MCG): every k-split plan covers
+    all input rows.  One token against the exact layer (C reconstruct); batches of 16 and 256 tokens (other k-split
+    plans, other modes: only fp32 summation order differs) within 1e-3 of per-token calls."""
+    from conftest import c_reconstruct
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(48)
+    E, H, I, K, top_k, cb = 128, 2048, 768, 3, 8, 1
+    st = {}
+    for proj, (kk, nn) in (("gate", (H, I)), ("up", (H, I)), ("down", (I, H))):
+        st[f"{proj}_trellis"] = torch.from_numpy(
+            rng.integers(-32768, 32768, size=(E, kk // 16, nn // 16, 16 * K), dtype=np.int16)).cuda()
+        st[f"{proj}_suh"] = torch.from_numpy(np.where(rng.random((E, kk)) < 0.5, -1.0, 1.0).astype(np.float16)).cuda()
+        st[f"{proj}_svh"] = torch.from_numpy(np.where(rng.random((E, nn)) < 0.5, -1.0, 1.0).astype(np.float16)).cuda()
+    T = 256
+    # scaled so that the fp16 intermediates of 2048- and 768-long sums of unit-size weights stay finite
+    x = torch.from_numpy((rng.standard_normal((T, H)) * 0.05).astype(np.float16)).cuda()
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32))
+    wsel, ids = torch.topk(logits, top_k, dim=1)
+    ids, w = ids.to(torch.int32).cuda(), torch.softmax(wsel, dim=1).cuda()
+
+    # one token against the exact layer
+    ids0 = ids[:1].cpu().numpy()
+    ex, cache = [None] * E, {}  # indexed by expert id (the oracle skips ids outside [0, len))
+    for e in set(ids0[0].tolist()):
+        ex[e] = {p: tuple(st[f"{p}_{part}"][e].cpu().numpy() for part in ("trellis", "suh", "svh"))
+                 for p in ("gate", "up", "down")}
+        for p in ("gate", "up", "down"):
+            cache[(e, p)] = c_reconstruct(coracle, ex[e][p][0], K, cb)
+    single = [ops.moe_forward(x[t:t + 1], ids[t:t + 1], w[t:t + 1], st, cb) for t in range(16)]
+    ref = orc.moe_forward(x[:1].cpu().numpy(), ids0, w[:1].cpu().numpy(), ex, K, cb, w_cache=cache)
+    nrel, mrel = _errs(single[0].cpu().numpy(), ref)
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+
+    y16 = ops.moe_forward(x[:16], ids[:16], w[:16], st, cb).float()
+    y256 = ops.moe_forward(x, ids, w, st, cb).float()
+    for t in range(16):
+        for y in (y16, y256):
+            d = (y[t] - single[t].float()).norm() / single[t].float().norm()
+            assert d.item() <= 1e-3, (t, y.shape[0], d.item())
+    for t in (100, 255):
+        one = ops.moe_forward(x[t:t + 1], ids[t:t + 1], w[t:t + 1], st, cb).float()
+        d = (y256[t] - one[0]).norm() / one[0].norm()
+        assert d.item() <= 1e-3, (t, d.item())
+
+
+@pytest.mark.parametrize("T", [3, 20, 40, 300])
+def test_moe_slot_groups_and_passes_match_exact_layer(T):
+    """Several tokens: routing launch, rotated inputs prepared once per slot, up to 16 P slots sharing each decoded
+    tile.  3 / 20 / 40 / 300 tokens over 8 experts run P = 1 / 2 / 4 / 4 groups (40 tokens: one pass of 40 slots per
+    expert in 3 groups; 300 tokens: 300 slots per expert, several passes).  Every token against the exact layer, and
+    two tokens against their single-token calls (slot mode: other k-split plan) within 1e-3."""
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(60 + T)
+    E, H, I, K, top_k = 8, 256, 256, 3, 8
+    ex = _experts(rng, E, H, I, K)
+    st = _stack(ex)
+    x = (rng.standard_normal((T, H)) * 0.5).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:top_k] for _ in range(T)]).astype(np.int32)
+    ids[0, 2] = -1
+    w = rng.random((T, top_k)).astype(np.float32)
+    xd, idd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    y = ops.moe_forward(xd, idd, wd, st, 1)
+    nrel, mrel = _errs(y.cpu().numpy(), orc.moe_forward(x, ids, w, ex, K, 1))
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+    for t in (0, T - 1):
+        one = ops.moe_forward(xd[t:t + 1], idd[t:t + 1], wd[t:t + 1], st, 1).float()[0]
+        assert ((y[t].float() - one).norm() / one.norm()).item() <= 1e-3, t
+    assert torch.equal(ops.moe_forward(xd, idd, wd, st, 1), y)

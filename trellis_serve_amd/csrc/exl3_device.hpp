@@ -29,6 +29,16 @@ typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 // 1/sqrt(128) as the reference kernels write it (cuda/csrc/exl3_marlin.cu:251)
 constexpr float kHadScale = 0.088388347648f;
 
+// fp16 of an fp32 product with two roundings, fp32 product then fp16, as the reference's __float2half_rn(a * b)
+// (here: the rotation scale, the SiLU product).  The empty asm keeps the fp32 product in a register: otherwise the backend may fuse multiply and conversion into
+// one v_fma_mixlo_f16 (a single rounding, one ulp apart in rare cases) in some expansions of an expression and not
+// in others, so two kernels evaluating the same expression could disagree.
+__device__ __forceinline__ _Float16 f16_of_f32(float p) {
+  __asm__("" : "+v"(p));
+  return (_Float16)p;
+}
+__device__ __forceinline__ _Float16 had_scale_f16(float f) { return f16_of_f32(f * kHadScale); }
+
 // s_waitcnt immediate for "vmcnt <= n" with expcnt and lgkmcnt unconstrained (gfx9 encoding: vmcnt bits 3:0 and
 // 15:14, expcnt 6:4, lgkmcnt 11:8)
 __host__ __device__ constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }

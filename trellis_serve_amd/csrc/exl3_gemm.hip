@@ -114,8 +114,8 @@ __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict
   float f0 = (float)(_Float16)(v[0] * sv.x), f1 = (float)(_Float16)(v[1] * sv.y);
   float f2 = (float)(_Float16)(v[2] * sv.z), f3 = (float)(_Float16)(v[3] * sv.w);
   had128_x4(f0, f1, f2, f3);
-  const _Float16 h[4] = {(_Float16)(f0 * kHadScale), (_Float16)(f1 * kHadScale), (_Float16)(f2 * kHadScale),
-                         (_Float16)(f3 * kHadScale)};
+  const _Float16 h[4] = {had_scale_f16(f0), had_scale_f16(f1), had_scale_f16(f2),
+                         had_scale_f16(f3)};
   // k-step major: the 32 halves of row r in k-step kt (one MFMA k-block) at [kt][r][32], so that one k-step of a row
   // block is one contiguous run and every 16-row A piece of the GEMM reads whole cache lines
   _Float16* dst = reinterpret_cast<_Float16*>(xh) + (size_t)s * rows * k;
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
       if (rotate_out) {
         const half8_t sv = sv8[q];
 #pragma unroll
-        for (int e = 0; e < 8; e++) o[e] = (_Float16)(v[8 * q + e] * kHadScale) * sv[e];
+        for (int e = 0; e < 8; e++) o[e] = had_scale_f16(v[8 * q + e]) * sv[e];
       } else {
 #pragma unroll
         for (int e = 0; e < 8; e++) o[e] = (_Float16)v[8 * q + e];

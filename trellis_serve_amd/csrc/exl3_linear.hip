@@ -58,10 +58,10 @@ __device__ __forceinline__ void had_in_4(const void* x_row, const uint16_t* __re
   float f0 = (float)(_Float16)(v[0] * su.x), f1 = (float)(_Float16)(v[1] * su.y);
   float f2 = (float)(_Float16)(v[2] * su.z), f3 = (float)(_Float16)(v[3] * su.w);
   had128_x4(f0, f1, f2, f3);
-  h[0] = (_Float16)(f0 * kHadScale);
-  h[1] = (_Float16)(f1 * kHadScale);
-  h[2] = (_Float16)(f2 * kHadScale);
-  h[3] = (_Float16)(f3 * kHadScale);
+  h[0] = had_scale_f16(f0);
+  h[1] = had_scale_f16(f1);
+  h[2] = had_scale_f16(f2);
+  h[3] = had_scale_f16(f3);
 }
 
 // output rotation of 4 fp16 values (lane t of a 32-lane group: block positions 4t..4t+3), then * svh
@@ -69,10 +69,10 @@ __device__ __forceinline__ void had_out_4(_Float16 h[4], const uint16_t* __restr
   float f0 = (float)h[0], f1 = (float)h[1], f2 = (float)h[2], f3 = (float)h[3];
   had128_x4(f0, f1, f2, f3);
   const half4_t sv = *reinterpret_cast<const half4_t*>(svh4);
-  h[0] = (_Float16)(f0 * kHadScale) * sv.x;
-  h[1] = (_Float16)(f1 * kHadScale) * sv.y;
-  h[2] = (_Float16)(f2 * kHadScale) * sv.z;
-  h[3] = (_Float16)(f3 * kHadScale) * sv.w;
+  h[0] = had_scale_f16(f0) * sv.x;
+  h[1] = had_scale_f16(f1) * sv.y;
+  h[2] = had_scale_f16(f2) * sv.z;
+  h[3] = had_scale_f16(f3) * sv.w;
 }
 
 template <bool BF16>

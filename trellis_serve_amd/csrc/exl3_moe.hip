@@ -8,21 +8,28 @@
 //   y[t] = sum_j w[t, j] * d[slot] in fp32, slot order, one rounding; slots whose expert id is outside [0, E) are
 //          skipped (exl3_marlin_moe.cu:274)
 //
-// Launches (the reference uses five plus an align launch; a single token skips the routing launch and runs its top-k
-// slots directly):
+// Launches (the reference uses five plus an align launch):
+//   single token (slot mode): moe_gemv_kernel<PHASE 0> -> moe_gemv_kernel<PHASE 1> -> moe_combine_kernel; grid row =
+//                      slot, its expert read from topk_ids, the rotations computed inside the expert workgroups.
+//   several tokens: moe_route_kernel -> moe_prep_kernel<0> -> moe_gemv_kernel<PHASE 0> -> moe_prep_kernel<1> ->
+//                      moe_gemv_kernel<PHASE 1> -> moe_combine_kernel; grid row = active expert, the rotated inputs
+//                      written once per slot by the prep launches and copied by the expert workgroups.
 //   moe_route_kernel   one workgroup: per-expert slot counts and lists (LDS atomics), the active experts in
 //                      ascending order.  The order of slots inside an expert's list does not change any result: the
 //                      rows of an MFMA are independent and the combine sums in slot order.
-//   moe_gemv_kernel<PHASE 0>  grid (2I/128 column blocks, active experts, k-splits): gate/up of every active expert
-//                      for all its slots, 16 slots per pass (TileStream, the dense GEMV's streaming core), input
-//                      rotation of x[token] with the shard's suh in the prologue, split-K reduce + output rotation
-//                      * svh by the last split, fp16 g|u rows.
-//   moe_gemv_kernel<PHASE 1>  same for down; the prologue computes a = fp16(silu(g) * u) and its rotation with
-//                      suh_down (the reference's separate GLU launch, fused).
+//   moe_prep_kernel    rotated gate/up inputs fp16(Had(x[token] * suh)) per (slot, shard), then the down inputs
+//                      fp16(Had(fp16(silu(g) * u) * suh_down)) per slot (the reference's moe_had_in and
+//                      moe_glu_had_in launches).
+//   moe_gemv_kernel<PHASE 0>  grid (2I/128 column blocks, experts or slots, k-splits): gate/up of every active expert
+//                      for all its slots on the dense GEMV's streaming core (TileStream); up to 16 P slots share each
+//                      decoded tile (P 16-row MFMAs); split-K reduce + output rotation * svh by the last split, fp16
+//                      g|u rows.
+//   moe_gemv_kernel<PHASE 1>  the same for down.
 //   moe_combine_kernel weighted fp32 sum over the token's slots.
 #include <stdlib.h>
 
 #include <algorithm>
+#include <cmath>
 
 #include "exl3_api.hpp"
 #include "exl3_device.hpp"
@@ -30,7 +37,7 @@
 
 namespace exl3 {
 
-constexpr int kMoeWaves = 8, kMoeThreads = kMoeWaves * 64, kMoeNT = 16;
+constexpr int kMoeWaves = 8, kMoeThreads = kMoeWaves * 64;
 constexpr int kMoeRows = 16;
 
 struct MoeArgs {
@@ -42,9 +49,14 @@ struct MoeArgs {
   const int* n_active;     // [1]
   const int* active;       // [E]: active experts, ascending
   const int* lists;        // [E][slots]
-  const int* topk_ids;     // [slots]: read directly in slot mode
+  const int* topk_ids;     // [slots]: read directly in slot mode and by the prep launches
   int slot_mode;           // 1: one workgroup row per slot, no routing launch (a single token: its top-k experts)
+  // rotated activations written once per slot by moe_prep_kernel (routed mode): gate/up inputs [2][slots][H], down
+  // inputs [slots][I], each 128-block in the staging order of a_slot
+  const uint16_t* pre_in;
+  const uint16_t* pre_dn;
 };
+
 
 __global__ __launch_bounds__(1024) void moe_route_kernel(const int* __restrict__ topk_ids, int slots, int E,
                                                          int* __restrict__ counts, int* __restrict__ n_active,
@@ -78,27 +90,93 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const int* __restrict__
   if (tid == 1023) *n_active = scan[1023];
 }
 
-// LDS: staged activations [16 rows][NT*16 + 4 halves], then per wave the stream stages; the epilogue reduce reuses it
-template <int K>
+// LDS: staged activations [16 P rows][NT*16 + 4 halves], then per wave the stream stages; the epilogue reduce reuses
+// it.  P groups of 16 slots share each decoded tile.
+template <int K, int P, int NT>
 __host__ __device__ constexpr int moe_lds_bytes() {
-  return kMoeRows * (kMoeNT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, kMoeNT>::LDS_BYTES > kMoeThreads * 16
-             ? kMoeRows * (kMoeNT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, kMoeNT>::LDS_BYTES
+  return kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, NT>::LDS_BYTES > kMoeThreads * 16
+             ? kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, NT>::LDS_BYTES
              : kMoeThreads * 16;
 }
 
+static_assert(moe_lds_bytes<8, 4, 16>() <= 160 * 1024, "MoE LDS must fit a CU");
+
 __device__ __forceinline__ float silu32(float v) { return v / (1.0f + __expf(-v)); }
 
-template <int K, int CB, int PHASE>
+// The rotated fp16 activations at positions kk .. kk+3 (kk = 128 b + 4 t, lane t of a half-wave) of one slot's input:
+// gate/up (PHASE 0): fp16(x[token] * suh) rotated; down (PHASE 1): a = fp16(silu(g) * u) (fp32 SiLU,
+// exl3_marlin_moe.cu:228-258), * suh, rotated.  One 128-block per half-wave (had128_x4 spans 32 lanes).
+template <int PHASE>
+__device__ __forceinline__ void moe_act4(const MoeArgs& a, const void* x, int x_bf16, const uint16_t* gu,
+                                         const uint16_t* suh, int slot, int kk, _Float16 h[4]) {
+  float f[4];
+  if constexpr (PHASE == 0) {
+    const uint16_t* xr = static_cast<const uint16_t*>(x) + (size_t)(slot / a.top_k) * a.H + kk;
+    _Float16 v[4];
+    if (x_bf16) {
+      const uint2_t raw = *reinterpret_cast<const uint2_t*>(xr);
+      v[0] = (_Float16)bf16_to_f32((uint16_t)(raw.x & 0xFFFF));
+      v[1] = (_Float16)bf16_to_f32((uint16_t)(raw.x >> 16));
+      v[2] = (_Float16)bf16_to_f32((uint16_t)(raw.y & 0xFFFF));
+      v[3] = (_Float16)bf16_to_f32((uint16_t)(raw.y >> 16));
+    } else {
+      const half4_t raw = *reinterpret_cast<const half4_t*>(xr);
+      v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+    }
+    const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
+    f[0] = (float)(_Float16)(v[0] * su.x); f[1] = (float)(_Float16)(v[1] * su.y);
+    f[2] = (float)(_Float16)(v[2] * su.z); f[3] = (float)(_Float16)(v[3] * su.w);
+  } else {
+    const half4_t gv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + kk);
+    const half4_t uv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + a.I + kk);
+    const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
+    f[0] = (float)(f16_of_f32(silu32((float)gv.x) * (float)uv.x) * su.x);
+    f[1] = (float)(f16_of_f32(silu32((float)gv.y) * (float)uv.y) * su.y);
+    f[2] = (float)(f16_of_f32(silu32((float)gv.z) * (float)uv.z) * su.z);
+    f[3] = (float)(f16_of_f32(silu32((float)gv.w) * (float)uv.w) * su.w);
+  }
+  had128_x4(f[0], f[1], f[2], f[3]);
+#pragma unroll
+  for (int i = 0; i < 4; i++) h[i] = had_scale_f16(f[i]);
+}
+
+// moe_prep_kernel<PHASE>: the rotated inputs of every routed slot, once (the reference's moe_had_in /
+// moe_glu_had_in launches, exl3_marlin_moe.cu:376-452): one half-wave per (slot, shard, 128-block); rows of
+// unrouted slots are left alone (never read).  Stored in the a_slot order so the GEMV stages them by plain copies.
+template <int PHASE>
+__global__ __launch_bounds__(256) void moe_prep_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
+                                                       const uint16_t* __restrict__ gu, uint16_t* __restrict__ pre) {
+  const int k = PHASE ? a.I : a.H;
+  const int kblocks = k >> 7, nsh = PHASE ? 1 : 2;
+  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (unit >= a.slots * nsh * kblocks) return;
+  const int t = threadIdx.x & 31;
+  const int b = unit % kblocks, rest = unit / kblocks;
+  const int sh = rest % nsh, slot = rest / nsh;
+  const int e = a.topk_ids[slot];
+  if (e < 0 || e >= a.E) return;
+  const uint16_t* suh = a.suh[PHASE ? 2 : sh] + (size_t)e * k;
+  _Float16 h[4];
+  moe_act4<PHASE>(a, x, x_bf16, gu, suh, slot, b * 128 + 4 * t, h);
+  // positions 4t, 4t+1 and 4t+2, 4t+3 land on adjacent staging slots: two 4-byte stores
+  _Float16* row = reinterpret_cast<_Float16*>(pre) + ((size_t)sh * a.slots + slot) * k;
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<half2_t*>(row + a_slot(b * 128 + 4 * t, 0, 0)) = half2_t{h[0], h[1]};
+  *reinterpret_cast<half2_t*>(row + a_slot(b * 128 + 4 * t + 2, 0, 0)) = half2_t{h[2], h[3]};
+}
+
+// PRE: activations copied from the prep launches' rows (routed mode); else computed here (slot mode, one row)
+template <int K, int CB, int PHASE, int P, bool PRE, int NT>
 __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
                                                                 uint16_t* __restrict__ gu, uint16_t* __restrict__ dn,
                                                                 float* __restrict__ partial,
-                                                                int* __restrict__ counters, int splits) {
-  typedef TileStream<K, CB, kMoeNT> Stream;
+                                                                int* __restrict__ counters, int splits, int chunks) {
+  typedef TileStream<K, CB, NT> Stream;
   constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
-  const int mstride = kMoeNT * 16 + 4;
+  const int mstride = NT * 16 + 4;
 
   // expert and its slots: routed mode -- grid row = active expert, its slot list from the routing launch; slot mode
   // -- grid row = slot, one slot, its expert read from topk_ids (split counters then index slots, so repeated experts
@@ -130,69 +208,73 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const 
   const uint32_t* trellis = a.tr[sh] + (size_t)e * (mat_bytes / 4);
   const uint16_t* suh = a.suh[sh] + (size_t)e * k;
   const uint16_t* svh = a.svh[sh] + (size_t)e * n_sh;
-  const int kb0 = sp * NB;
-  const int nb = min(k >> 7, kb0 + NB) - kb0;
+  const uint16_t* pre = PRE ? (PHASE ? a.pre_dn : a.pre_in + (size_t)sh * a.slots * k) : nullptr;
+  // this split's k range: `chunks` chunks of NB 128-row blocks, from chunk sp * chunks (the last split may hold fewer)
+  const int kblocks = k >> 7;
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
   const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
-  uint8_t* stage = lds + kMoeRows * mstride * 2 + w * Stream::LDS_BYTES;
+  uint8_t* stage = lds + kMoeRows * P * mstride * 2 + w * Stream::LDS_BYTES;
 
-  for (int c0 = 0; c0 < n_e; c0 += kMoeRows) {
-    const int M = min(kMoeRows, n_e - c0);
-    Stream stream;
-    stream.init(trellis, mat_bytes, tn, cbl * kMoeWaves + w, kb0, nb, stage, l);
-    stream.start();
-    for (int u = hw; u < M * NB; u += 2 * kMoeWaves) {
-      const int m = u / NB, b = u - m * NB;
-      const int kk = (kb0 + b) * 128 + 4 * t;
-      const int slot = slot_at(c0 + m);
-      _Float16 h[4] = {0, 0, 0, 0};
-      if (b < nb) {
-        float f[4];
-        if constexpr (PHASE == 0) {
-          const uint16_t* xr = static_cast<const uint16_t*>(x) + (size_t)(slot / a.top_k) * a.H + kk;
-          _Float16 v[4];
-          if (x_bf16) {
-            const uint2_t raw = *reinterpret_cast<const uint2_t*>(xr);
-            v[0] = (_Float16)bf16_to_f32((uint16_t)(raw.x & 0xFFFF));
-            v[1] = (_Float16)bf16_to_f32((uint16_t)(raw.x >> 16));
-            v[2] = (_Float16)bf16_to_f32((uint16_t)(raw.y & 0xFFFF));
-            v[3] = (_Float16)bf16_to_f32((uint16_t)(raw.y >> 16));
-          } else {
-            const half4_t raw = *reinterpret_cast<const half4_t*>(xr);
-            v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
-          }
-          const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
-          f[0] = (float)(_Float16)(v[0] * su.x); f[1] = (float)(_Float16)(v[1] * su.y);
-          f[2] = (float)(_Float16)(v[2] * su.z); f[3] = (float)(_Float16)(v[3] * su.w);
-        } else {
-          const half4_t gv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + kk);
-          const half4_t uv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + a.I + kk);
-          const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
-          f[0] = (float)((_Float16)(silu32((float)gv.x) * (float)uv.x) * su.x);
-          f[1] = (float)((_Float16)(silu32((float)gv.y) * (float)uv.y) * su.y);
-          f[2] = (float)((_Float16)(silu32((float)gv.z) * (float)uv.z) * su.z);
-          f[3] = (float)((_Float16)(silu32((float)gv.w) * (float)uv.w) * su.w);
+  // passes of up to 16 P slots; each decoded tile feeds the pass's `groups` 16-row MFMAs
+  for (int c0 = 0; c0 < n_e; c0 += kMoeRows * P) {
+    const int M = min(kMoeRows * P, n_e - c0);
+    const int groups = (M + kMoeRows - 1) / kMoeRows;
+    float4_t acc[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) acc[p] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int ch = 0; ch < chunks; ch++) {
+      const int kb0 = (sp * chunks + ch) * NB;
+      if (kb0 >= kblocks) break;
+      const int nb = min(kblocks, kb0 + NB) - kb0;
+      Stream stream;
+      stream.init(trellis, mat_bytes, tn, cbl * kMoeWaves + w, kb0, nb, stage, l);
+      stream.start();
+      if constexpr (PRE) {
+        // precomputed rows: 128-block copies (8 bytes per lane), all loads of the half-wave issued before the stores
+        constexpr int IT = kMoeRows * P * NB / (2 * kMoeWaves);
+        uint2_t v[IT];
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+          const int u = hw + it * 2 * kMoeWaves;
+          const int m = u / NB, b = u - m * NB;
+          v[it] = uint2_t{0u, 0u};
+          if (u < M * NB && b < nb)
+            v[it] = *reinterpret_cast<const uint2_t*>(pre + (size_t)slot_at(c0 + m) * k + (kb0 + b) * 128 + 4 * t);
         }
-        had128_x4(f[0], f[1], f[2], f[3]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) h[i] = (_Float16)(f[i] * kHadScale);
+        for (int it = 0; it < IT; it++) {
+          const int u = hw + it * 2 * kMoeWaves;
+          const int m = u / NB, b = u - m * NB;
+          if (u < M * NB) *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
+        }
+      } else {
+        for (int u = hw; u < M * NB; u += 2 * kMoeWaves) {
+          const int m = u / NB, b = u - m * NB;
+          _Float16 h[4] = {0, 0, 0, 0};
+          if (b < nb) moe_act4<PHASE>(a, x, x_bf16, gu, suh, slot_at(c0 + m), (kb0 + b) * 128 + 4 * t, h);
+#pragma unroll
+          for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
+        }
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
+      __syncthreads();
+      // A row of lane group c in group p: 16 p + c (group 0: min(c, M - 1)); rows >= M feed only C rows never stored
+      stream.template run_groups<P>(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j,
+                                    kMoeRows * mstride / 4, groups, acc);
+      __syncthreads();  // the next chunk or pass restages LDS
     }
-    __syncthreads();
-    const float4_t acc = stream.run(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j);
     // this split's partial rows, device-coherent (read by the last split, possibly on another XCD)
     float* pdst = partial + (size_t)sp * a.slots * n_out + cb * 128 + w * 16 + c;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int m = 4 * j + r;
-      if (m < M)
-        __hip_atomic_store(pdst + (size_t)slot_at(c0 + m) * n_out, acc[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();  // the next pass restages LDS
+    for (int p = 0; p < P; p++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = kMoeRows * p + 4 * j + r;
+        if (m < M)
+          __hip_atomic_store(pdst + (size_t)slot_at(c0 + m) * n_out, acc[p][r], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
@@ -223,19 +305,24 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const 
     float f0 = (float)h[0], f1 = (float)h[1], f2 = (float)h[2], f3 = (float)h[3];
     had128_x4(f0, f1, f2, f3);
     const half4_t sv = *reinterpret_cast<const half4_t*>(svh + cbl * 128 + 4 * t);
-    const half4_t o = {(_Float16)((_Float16)(f0 * kHadScale) * sv.x), (_Float16)((_Float16)(f1 * kHadScale) * sv.y),
-                       (_Float16)((_Float16)(f2 * kHadScale) * sv.z), (_Float16)((_Float16)(f3 * kHadScale) * sv.w)};
+    const half4_t o = {(_Float16)(had_scale_f16(f0) * sv.x), (_Float16)(had_scale_f16(f1) * sv.y),
+                       (_Float16)(had_scale_f16(f2) * sv.z), (_Float16)(had_scale_f16(f3) * sv.w)};
     *reinterpret_cast<half4_t*>(out + (size_t)slot * n_out + col) = o;
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(&counters[ctr_row * (n_out / 128) + cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// y[tok, cols] = sum over the token's valid slots, in slot order, of w * dn[slot, cols] in fp32, one rounding
+// (exl3_marlin_moe.cu:262-292).  One half-wave per (token, 128-column block), 4 columns per lane.  The slots are taken
+// 8 at a time: their ids, weights and rows are loaded together (one memory round trip per 8 slots instead of a
+// dependent chain per slot); a skipped slot leaves the sum untouched, exactly as if it were not visited.
 template <bool Y_BF16>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ dn,
                                                           const int* __restrict__ topk_ids,
                                                           const float* __restrict__ topk_w, int tokens, int top_k,
                                                           int E, int H, void* __restrict__ y) {
+  constexpr int kChunk = 8;
   const int nb = H >> 7;
   const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
   if (unit >= tokens * nb) return;
@@ -243,16 +330,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   const int tok = unit / nb, b = unit - tok * nb;
   const int col = b * 128 + 4 * t;
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int jj = 0; jj < top_k; jj++) {
-    const int slot = tok * top_k + jj;
-    const int e = topk_ids[slot];
-    if (e < 0 || e >= E) continue;
-    const float wgt = topk_w[slot];
-    const half4_t v = *reinterpret_cast<const half4_t*>(dn + (size_t)slot * H + col);
-    acc.x += wgt * (float)v.x;
-    acc.y += wgt * (float)v.y;
-    acc.z += wgt * (float)v.z;
-    acc.w += wgt * (float)v.w;
+  for (int j0 = 0; j0 < top_k; j0 += kChunk) {
+    bool use[kChunk];
+    float wgt[kChunk];
+    half4_t v[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; i++) {
+      const int slot = tok * top_k + min(j0 + i, top_k - 1);
+      const int e = topk_ids[slot];
+      use[i] = j0 + i < top_k && e >= 0 && e < E;
+      wgt[i] = topk_w[slot];
+      v[i] = *reinterpret_cast<const half4_t*>(dn + (size_t)slot * H + col);  // in bounds; unused unless use[i]
+    }
+#pragma unroll
+    for (int i = 0; i < kChunk; i++) {
+      if (use[i]) {
+        acc.x = __builtin_fmaf(wgt[i], (float)v[i].x, acc.x);
+        acc.y = __builtin_fmaf(wgt[i], (float)v[i].y, acc.y);
+        acc.z = __builtin_fmaf(wgt[i], (float)v[i].z, acc.z);
+        acc.w = __builtin_fmaf(wgt[i], (float)v[i].w, acc.w);
+      }
+    }
   }
   uint16_t* yr = static_cast<uint16_t*>(y) + (size_t)tok * H + col;
   if constexpr (Y_BF16) {
@@ -267,25 +365,51 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
 
 // ---- host ----------------------------------------------------------------------------------------------------------
 
+// k-split plan of one expert GEMV phase: a chunk is NB = NT/8 blocks of 128 input rows; the C chunks of k are
+// dealt to `splits` workgroups of `chunks` consecutive chunks each.  The split count is the smallest that gives about
+// 2048 working workgroups (more splits only add per-workgroup fixed costs and partials: measured at 1, 16 and 256
+// tokens), and at most what keeps the fp32 partials (written and read once per slot, output column and split)
+// within a quarter of the expert weight bytes streamed.  rows: grid rows that do work (active experts, or slots).
+struct MoePhase {
+  int splits, chunks;
+};
+
+static MoePhase moe_phase_plan(int slots, int rows, int nblk, int k, int K, int nt) {
+  const int NB = nt / 8;
+  const int C = (k / 128 + NB - 1) / NB;
+  const double per_split = (double)slots * 8.0 / ((double)rows * k * std::max(K, 1) / 8.0);
+  const int cap = std::max(1, (int)(0.25 / per_split));
+  const int want = std::max(1, (2048 + rows * nblk - 1) / (rows * nblk));
+  const int s = std::min(C, std::min(cap, want));
+  MoePhase ph{};
+  ph.chunks = (C + s - 1) / s;
+  ph.splits = (C + ph.chunks - 1) / ph.chunks;
+  return ph;
+}
+
 struct MoePlan {
-  int splits_gu, splits_dn;
-  size_t off_counts, off_nactive, off_active, off_lists, off_gu, off_dn, off_cnt_gu, off_cnt_dn, off_partial, total;
+  bool slot_mode;  // a single token: grid rows = its slots, no routing or prep launches
+  int groups;      // P: 16-slot groups per pass over an expert's weights (1, 2 or 4)
+  int nt;          // tile rows per chunk
+  MoePhase gu, dn;
+  size_t off_counts, off_nactive, off_active, off_lists, off_gu, off_dn, off_cnt_gu, off_cnt_dn, off_pre_in,
+      off_pre_dn, off_partial, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-static int moe_splits(int slots, int E, int nblk, int k) {
-  const int active = std::max(1, std::min(E, slots));
-  const int want = (1536 + active * nblk - 1) / (active * nblk);
-  const int maxs = (k / 128 + (kMoeNT / 8) - 1) / (kMoeNT / 8);
-  return std::max(1, std::min(want, maxs));
-}
-
-static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I) {
+static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I, int K) {
   MoePlan p{};
   const int slots = tokens * top_k;
-  p.splits_gu = moe_splits(slots, E, 2 * I / 128, H);
-  p.splits_dn = moe_splits(slots, E, H / 128, I);
+  p.slot_mode = tokens == 1 && slots <= E;
+  const int rows = p.slot_mode ? slots : std::max(1, std::min(E, slots));
+  p.nt = 16;  // 32 measured slower with 256 tokens, equal with 16
+  p.gu = moe_phase_plan(slots, rows, 2 * I / 128, H, K, p.nt);
+  p.dn = moe_phase_plan(slots, rows, H / 128, I, K, p.nt);
+  // enough groups that an expert with a typical-to-high slot count (mean + ~2.5 sd of a binomial count) is one pass
+  const double mean = (double)slots / rows;
+  const double high = mean + 2.5 * std::sqrt(mean);
+  p.groups = p.slot_mode || high <= 16 ? 1 : high <= 32 ? 2 : 4;
   // the split counters first, in the fixed counter region (zero between calls whatever the shapes)
   p.off_cnt_gu = 0;
   p.off_cnt_dn = (size_t)E * (2 * I / 128) * 4;
@@ -296,10 +420,30 @@ static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I) {
   p.off_lists = o; o = align256(o + (size_t)E * slots * 4);
   p.off_gu = o; o = align256(o + (size_t)slots * 2 * I * 2);
   p.off_dn = o; o = align256(o + (size_t)slots * H * 2);
+  p.off_pre_in = o; o = align256(o + (p.slot_mode ? 0 : (size_t)2 * slots * H * 2));
+  p.off_pre_dn = o; o = align256(o + (p.slot_mode ? 0 : (size_t)slots * I * 2));
   p.off_partial = o;
-  o = align256(o + std::max((size_t)p.splits_gu * slots * 2 * I, (size_t)p.splits_dn * slots * H) * 4);
+  o = align256(o + std::max((size_t)p.gu.splits * slots * 2 * I, (size_t)p.dn.splits * slots * H) * 4);
   p.total = o;
   return p;
+}
+
+template <int K, int CB, int PHASE>
+static void launch_moe_gemv(const MoePlan& p, const MoePhase& ph, dim3 grid, const MoeArgs& a, const void* x,
+                            int x_bf16, uint16_t* gu, uint16_t* dn, float* partial, int* counters, hipStream_t st) {
+  const dim3 g3(grid.x, grid.y, ph.splits);
+#define EXL3_MOE_GEMV(P_, PRE_, NT_)                                                                         \
+  moe_gemv_kernel<K, CB, PHASE, P_, PRE_, NT_><<<g3, kMoeThreads, moe_lds_bytes<K, P_, NT_>(), st>>>(        \
+      a, x, x_bf16, gu, dn, partial, counters, ph.splits, ph.chunks)
+  if (p.slot_mode)
+    EXL3_MOE_GEMV(1, false, 16);
+  else if (p.groups == 4)
+    EXL3_MOE_GEMV(4, true, 16);
+  else if (p.groups == 2)
+    EXL3_MOE_GEMV(2, true, 16);
+  else
+    EXL3_MOE_GEMV(1, true, 16);
+#undef EXL3_MOE_GEMV
 }
 
 #define EXL3_MOE_DISPATCH(K_, CB_, ...)                                   \
@@ -321,10 +465,9 @@ static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I) {
 using namespace exl3;
 
 extern "C" size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K) {
-  (void)K;
   if (tokens <= 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || inter <= 0) return 0;
   if ((int64_t)num_experts * (2 * inter + hidden) / 128 > kMaxCounters) return 0;
-  return moe_plan(tokens, top_k, num_experts, hidden, inter).total;
+  return moe_plan(tokens, top_k, num_experts, hidden, inter, K).total;
 }
 
 extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids,
@@ -347,7 +490,7 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   if (tokens == 0) return EXL3_OK;
   const int slots = tokens * top_k;
   EXL3_CHECK_ARG((int64_t)slots * std::max(2 * inter, hidden) <= INT32_MAX / 4, "exl3_moe_forward: too many slots");
-  const MoePlan p = moe_plan(tokens, top_k, num_experts, hidden, inter);
+  const MoePlan p = moe_plan(tokens, top_k, num_experts, hidden, inter, K);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= p.total, "exl3_moe_forward: workspace %zu bytes, need %zu",
                  workspace_bytes, p.total);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -375,26 +518,33 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   a.active = active;
   a.lists = lists;
   a.topk_ids = static_cast<const int*>(topk_ids);
-  // a single token: its top-k slots run directly (no routing launch); several tokens share experts, so they are routed
-  a.slot_mode = tokens == 1 && slots <= num_experts;
+  a.slot_mode = p.slot_mode;
   uint16_t* gu = reinterpret_cast<uint16_t*>(ws + p.off_gu);
   uint16_t* dn = reinterpret_cast<uint16_t*>(ws + p.off_dn);
   int* cnt_gu = reinterpret_cast<int*>(ws + p.off_cnt_gu);
   int* cnt_dn = reinterpret_cast<int*>(ws + p.off_cnt_dn);
+  uint16_t* pre_in = reinterpret_cast<uint16_t*>(ws + p.off_pre_in);
+  uint16_t* pre_dn = reinterpret_cast<uint16_t*>(ws + p.off_pre_dn);
   float* partial = reinterpret_cast<float*>(ws + p.off_partial);
+  a.pre_in = pre_in;
+  a.pre_dn = pre_dn;
   hipStream_t st = as_stream(stream);
 
   if (!a.slot_mode) {
     moe_route_kernel<<<1, 1024, 0, st>>>(static_cast<const int*>(topk_ids), slots, num_experts, counts, nactive,
                                          active, lists);
     EXL3_CHECK_LAUNCH();
+    moe_prep_kernel<0><<<(unsigned)(((size_t)slots * 2 * (hidden / 128) + 7) / 8), 256, 0, st>>>(a, x, x_bf16, gu,
+                                                                                                  pre_in);
+    EXL3_CHECK_LAUNCH();
   }
-  const int max_active = a.slot_mode ? slots : std::min(num_experts, slots);
+  const int rows = a.slot_mode ? slots : std::min(num_experts, slots);
   bool ok = EXL3_MOE_DISPATCH(K, codebook, {
-    moe_gemv_kernel<kK, kCB, 0><<<dim3(2 * inter / 128, max_active, p.splits_gu), kMoeThreads, moe_lds_bytes<kK>(),
-                                  st>>>(a, x, x_bf16, gu, dn, partial, cnt_gu, p.splits_gu);
-    moe_gemv_kernel<kK, kCB, 1><<<dim3(hidden / 128, max_active, p.splits_dn), kMoeThreads, moe_lds_bytes<kK>(),
-                                  st>>>(a, x, x_bf16, gu, dn, partial, cnt_dn, p.splits_dn);
+    launch_moe_gemv<kK, kCB, 0>(p, p.gu, dim3(2 * inter / 128, rows), a, x, x_bf16, gu, dn, partial, cnt_gu, st);
+    if (!a.slot_mode)
+      moe_prep_kernel<1><<<(unsigned)(((size_t)slots * (inter / 128) + 7) / 8), 256, 0, st>>>(a, x, x_bf16, gu,
+                                                                                              pre_dn);
+    launch_moe_gemv<kK, kCB, 1>(p, p.dn, dim3(hidden / 128, rows), a, x, x_bf16, gu, dn, partial, cnt_dn, st);
   });
   if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_moe_forward: unsupported K/codebook");
   EXL3_CHECK_LAUNCH();

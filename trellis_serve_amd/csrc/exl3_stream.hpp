@@ -95,6 +95,30 @@ struct TileStream {
     }
     return acc0 + acc1;
   }
+
+  // For up to P groups of 16 A rows sharing each decoded tile (groups <= P active, uniform): group p reads its
+  // fragment gstride half4 after group p-1's and accumulates into acc[p] (one chain per group: the decode between two
+  // MFMAs of a group covers their dependency).
+  template <int P>
+  __device__ __forceinline__ void run_groups(const half4_t* ap, int gstride, int groups, float4_t (&acc)[P]) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      uint8_t* st = stage + (b & 1) * STAGE;
+#pragma unroll
+      for (int i = 0; i < LPB; i++)
+        if (glive[i]) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
+      if (b + 3 < NB) issue(b + 3);
+      const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const half4_t bv = decode_group<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
+#pragma unroll
+        for (int p = 0; p < P; p++)
+          if (p == 0 || p < groups)
+            acc[p] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[p * gstride + (b * 8 + u) * 4], bv, acc[p], 0, 0, 0);
+      }
+    }
+  }
 };
 
 // A-operand staging in LDS: position p of the k-range, row m -> [m][p/16][q][e] with r = p % 16, q = (r & 7) >> 1,
