@@ -1,0 +1,70 @@
+"""The fused kernels at the benchmark's own shapes (BASELINE configs[1] and [2]), where the split plans, tail tiles
+and shard maps take the forms the small parity shapes never reach.  The reference output is built on the GPU from
+pieces pinned elsewhere: the bit-exact reconstruct (W_inner), the input rotation (1-ulp fp16 agreement with the
+oracle) and an fp32 matmul, then the output rotation; the fused result must agree within the north-star tolerance
+(norm-relative and max-relative 2e-3)."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _ops():
+    from trellis_serve_amd import ops
+    return ops
+
+
+def _layer(g, k, ns, K):
+    trs = [torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=torch.int16, generator=g).cuda() for n in ns]
+    suhs = [(torch.randint(0, 2, (k,), generator=g) * 2 - 1).half().cuda() for _ in ns]
+    svhs = [(torch.randint(0, 2, (n,), generator=g) * 2 - 1).half().cuda() for n in ns]
+    return trs, suhs, svhs
+
+
+def _reference(x, trs, suhs, svhs, cb):
+    """had(had(x * suh) @ W_inner) * svh per shard: rotation kernels + reconstruct + fp32 matmul."""
+    ops = _ops()
+    M = x.shape[0]
+    out = torch.empty((M, sum(t.shape[1] * 16 for t in trs)), dtype=torch.float16, device=x.device)
+    col = 0
+    for tr, suh, svh in zip(trs, suhs, svhs):
+        xh = ops.had_in_group(x, suh)
+        w = ops.reconstruct(tr, cb)
+        y = (xh.float() @ w.float()).half()
+        ops.had_out_into(y, svh, out, col)
+        col += w.shape[1]
+        del w
+    return out
+
+
+def _check(y, ref):
+    y, ref = y.float(), ref.float()
+    nrel = ((y - ref).norm() / ref.norm()).item()
+    mrel = ((y - ref).abs().max() / ref.abs().max()).item()
+    assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
+
+
+C2_LAYERS = {"qkv": (5120, [6144, 1024, 1024]), "o": (6144, [5120]), "gate_up": (5120, [17408, 17408]),
+             "down": (17408, [5120])}
+
+
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("name", list(C2_LAYERS))
+def test_gemv_c2_layer_set_shapes(name, M):
+    """the four fused K = 3 MCG linears of the 27B-class layer set at M = 1 and 16."""
+    g = torch.Generator(device="cpu").manual_seed(100 + M)
+    k, ns = C2_LAYERS[name]
+    trs, suhs, svhs = _layer(g, k, ns, 3)
+    x = torch.randn((M, k), generator=g).half().cuda()
+    _check(_ops().linear(x, trs, suhs, svhs, 1), _reference(x, trs, suhs, svhs, 1))
+
+
+@pytest.mark.parametrize("K,cb,M", [(3, 1, 2048), (2, 0, 512), (8, 2, 512)])
+def test_prefill_c3_shape(K, cb, M):
+    """the 5120 -> 17408 prefill decode-GEMM (68 column tiles, split-K tail items) at the benchmark's K,
+    codebook and row counts."""
+    g = torch.Generator(device="cpu").manual_seed(200 + K)
+    trs, suhs, svhs = _layer(g, 5120, [17408], K)
+    x = (torch.randn((M, 5120), generator=g) * 0.5).half().cuda()
+    _check(_ops().linear_prefill(x, trs, suhs, svhs, cb), _reference(x, trs, suhs, svhs, cb))
