@@ -120,16 +120,36 @@ def test_linear_c1_shape_4096(coracle):
     assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
 
 
-def test_linear_bf16_boundary_equals_fp16_casts():
-    """run(x_bf16) == run(x_bf16.half()).bfloat16() bit for bit (cuda/src/sglang_exl3/parity/marlin_parity.py:98-111)."""
+@pytest.mark.parametrize("rows,k,n", [(4, 512, 384), (16, 4096, 16384)])
+def test_linear_bf16_boundary_equals_fp16_casts(rows, k, n):
+    """run(x_bf16) == run(x_bf16.half()).bfloat16() bit for bit (cuda/src/sglang_exl3/parity/marlin_parity.py:98-111);
+    16 rows of a 4096 -> 16384 linear take the path that rotates the input once per shard before the GEMV."""
     rng = np.random.default_rng(5)
-    k, n, K, cb = 512, 384, 3, 1
+    K, cb = 3, 1
     tr, suh, svh = _dev(_trellis(rng, k, n, K)), _dev(_signs(rng, k)), _dev(_signs(rng, n))
-    x = torch.from_numpy(rng.standard_normal((4, k)).astype(np.float32)).cuda().bfloat16()
+    x = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float32)).cuda().bfloat16()
     y_bf = _ops().linear(x, [tr], [suh], [svh], cb)
     y_h = _ops().linear(x.half(), [tr], [suh], [svh], cb)
     assert y_bf.dtype == torch.bfloat16
     assert torch.equal(y_bf, y_h.bfloat16())
+
+
+def test_linear_rows_rotated_once_match_rows_rotated_per_workgroup():
+    """With 8+ rows and enough column blocks x rows x k-blocks (here 128 x 16 x 32), the input rotation runs once per
+    shard (fragment-order rows) before the GEMV; a 16-row call must agree with 4-row calls (rotation inside every
+    workgroup) to rounding: the split-K reduce groups its fp32 partials by row count (16 rows: one sequential sum;
+    4 rows: 4 interleaved sums, then their sum), so results are bit-identical per shape, not across row counts."""
+    rng = np.random.default_rng(6)
+    k, K, cb = 4096, 3, 1
+    ns = (8192, 8192)
+    cases = [(_dev(_trellis(rng, k, n, K)), _dev(_signs(rng, k)), _dev(_signs(rng, n))) for n in ns]
+    args = ([c[0] for c in cases], [c[1] for c in cases], [c[2] for c in cases], cb)
+    x = torch.from_numpy((rng.standard_normal((16, k)) * 0.5).astype(np.float16)).cuda()
+    y16 = _ops().linear(x, *args)
+    y4 = torch.cat([_ops().linear(x[r:r + 4].contiguous(), *args) for r in range(0, 16, 4)])
+    d = (y16.float() - y4.float()).norm() / y4.float().norm()
+    assert d.item() <= 1e-4, d.item()
+    assert torch.equal(_ops().linear(x, *args), y16)
 
 
 def test_linear_fused_group_matches_oracle_per_shard(coracle):

@@ -123,6 +123,27 @@ __global__ __launch_bounds__(256) void had_in_kernel(const void* __restrict__ x,
   store_4<false>(xh + ((size_t)s * rows + r) * k, kk, h);
 }
 
+// The rotated activations of every shard of a fused linear, xh[s][r][k] = fp16(Had(x[r] * suh_s)), each 16-position
+// group stored in the GEMV's A-staging order (a_slot) so that gemv_kernel<.., PRE> stages rows by plain copies.  One
+// half-wave per (shard, row, 128-block).
+template <bool X_BF16>
+__global__ __launch_bounds__(256) void had_in_shards_kernel(const void* __restrict__ x, int rows, int k, ShardArgs sa,
+                                                            uint16_t* __restrict__ xh) {
+  const int kb = k >> 7;
+  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (unit >= sa.count * rows * kb) return;
+  const int t = threadIdx.x & 31;
+  const int s = unit / (rows * kb), rem = unit - s * rows * kb, r = rem / kb, b = rem - r * kb;
+  const int kk = b * 128 + 4 * t;
+  _Float16 h[4];
+  had_in_4<X_BF16>(static_cast<const uint16_t*>(x) + (size_t)r * k, sa.suh[s], kk, h);
+  // positions 4t, 4t+1 and 4t+2, 4t+3 land on adjacent staging slots: two 4-byte stores
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  _Float16* row = reinterpret_cast<_Float16*>(xh) + ((size_t)s * rows + r) * k;
+  *reinterpret_cast<half2_t*>(row + a_slot(kk, 0, 0)) = half2_t{h[0], h[1]};
+  *reinterpret_cast<half2_t*>(row + a_slot(kk + 2, 0, 0)) = half2_t{h[2], h[3]};
+}
+
 template <bool OUT_BF16>
 __global__ __launch_bounds__(256) void had_out_kernel(const uint16_t* __restrict__ y, int rows, int n,
                                                       const uint16_t* __restrict__ svh, void* __restrict__ out,
@@ -170,11 +191,13 @@ __host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K) {
              : kGemvThreads * 16;
 }
 
-template <int K, int CB, bool ROTATE, int NT>
+// PRE: x is the rotated activations of every shard, [shards][pre_rows][k] in A-staging order (had_in_kernel<.., true>),
+// staged by plain 8-byte copies; else x is the input rows, rotated here (ROTATE) or taken as given
+template <int K, int CB, bool ROTATE, int NT, bool PRE = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
                                                              int M, int k, int splits, float* __restrict__ partial,
                                                              int* __restrict__ counters, void* __restrict__ y,
-                                                             int y_bf16, int n_total) {
+                                                             int y_bf16, int n_total, int pre_rows = 0) {
   typedef TileStream<K, CB, NT> Stream;
   constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -195,7 +218,26 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   stream.start();
 
   // prologue: activations of the split, rotated (or as given), into LDS; blocks past the split's end are zero
-  {
+  if constexpr (PRE) {
+    // one (row, block) unit per half-wave, 8 bytes per lane; all loads of the half-wave issued before the stores
+    constexpr int IT = kGemvRows * NB / (2 * kGemvWaves);
+    const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
+    const uint16_t* pre = static_cast<const uint16_t*>(x) + (size_t)s * pre_rows * k;
+    uint2_t v[IT];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+      const int u = hw + it * 2 * kGemvWaves;
+      const int m = u / NB, b = u - m * NB;
+      v[it] = uint2_t{0u, 0u};
+      if (u < M * NB && b < nb) v[it] = *reinterpret_cast<const uint2_t*>(pre + (size_t)m * k + (kb0 + b) * 128 + 4 * t);
+    }
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+      const int u = hw + it * 2 * kGemvWaves;
+      const int m = u / NB, b = u - m * NB;
+      if (u < M * NB) *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
+    }
+  } else {
     const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
     for (int u = hw; u < M * NB; u += 2 * kGemvWaves) {
       const int m = u / NB, b = u - m * NB;
@@ -364,20 +406,60 @@ static int build_shards(const exl3_shard* shards, int nshards, int k, int K, Sha
 }
 
 // one launch per 16 rows: decode-GEMV + in-launch split reduce (+ rotations when `rotate`)
+// With many rows and much redundant rotation work (every column block's workgroup rotates the rows of its split:
+// nblk x rows x k/128 half-wave units in total), the input rotation runs once per shard and row (had_in_shards_kernel)
+// before the GEMV.  At M = 16 the per-workgroup rotation made the gate_up launch of the layer set LDS-bound (its
+// shuffles and scattered staging writes): 51 us against 41 us with the separate rotation, 34 us at M = 1; for the
+// q/k/v and o launches (under 65536 units) the extra launch costs more than it saves.
+constexpr int kGemvPreRows = 8;
+constexpr size_t kGemvPreUnits = 65536;
+
+static bool gemv_pre(int rows, int k, int n_total) {
+  return rows >= kGemvPreRows && (size_t)(n_total / 128) * rows * (k / 128) >= kGemvPreUnits;
+}
+
+// workspace layout: [counter region][fp32 partials of the largest 16-row launch][rotated rows, when gemv_pre]
+static size_t gemv_partial_bytes(int rows, int k, int n_total, int K) {
+  size_t need = 0;
+  for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
+    if (M == 0) continue;
+    const GemvPlan pl = gemv_plan(k, n_total, M, K);
+    need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
+  }
+  return (need + 255) & ~(size_t)255;
+}
+static size_t gemv_pre_bytes(int rows, int k, int n_total) {
+  return gemv_pre(rows, k, n_total) ? (size_t)EXL3_MAX_SHARDS * rows * k * 2 : 0;
+}
+
 static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_bf16, int rows, int k, int K, int cb,
                        int n_total, void* workspace, void* y, bool y_bf16, hipStream_t st) {
   int* counters = static_cast<int*>(workspace);
   float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total));
+  const bool pre = rotate && gemv_pre(rows, k, n_total);
+  uint16_t* xh = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total) +
+                                             gemv_partial_bytes(rows, k, n_total, K));
+  if (pre) {
+    const dim3 hgrid((unsigned)(((size_t)sa.count * rows * (k / 128) + 7) / 8));
+    if (x_bf16)
+      had_in_shards_kernel<true><<<hgrid, 256, 0, st>>>(x, rows, k, sa, xh);
+    else
+      had_in_shards_kernel<false><<<hgrid, 256, 0, st>>>(x, rows, k, sa, xh);
+    EXL3_CHECK_LAUNCH();
+  }
   for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
     const int M = std::min(kGemvRows, rows - r0);
     const GemvPlan pl = gemv_plan(k, n_total, M, K);
     const dim3 grid(n_total / 128, pl.splits);
-    const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * k * 2;
+    const void* xr = static_cast<const uint8_t*>(pre ? (const void*)xh : x) + (size_t)r0 * k * 2;
     void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
     bool ok = false;
 #define EXL3_GEMV_LAUNCH(NTV)                                                                                        \
   if (pl.nt == NTV) {                                                                                                \
-    if (rotate)                                                                                                      \
+    if (pre)                                                                                                         \
+      ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, NTV, true><<<grid, kGemvThreads, pl.lds, st>>>(    \
+          sa, xr, 0, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows)));                          \
+    else if (rotate)                                                                                                 \
       ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, NTV><<<grid, kGemvThreads, pl.lds, st>>>(           \
           sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
     else                                                                                                             \
@@ -451,14 +533,8 @@ extern "C" int exl3_had_out_into(const void* y, int rows, int n, const void* svh
 extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K) {
   (void)K;
   if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128 || n_total / 128 > kMaxCounters) return 0;
-  // launches take 16 rows at a time, then the remainder: the workspace must hold either plan's partials
-  size_t need = 0;
-  for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
-    if (M == 0) continue;
-    const GemvPlan pl = gemv_plan(k, n_total, M, K);
-    need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
-  }
-  return counters_bytes(n_total) + need;
+  // launches take 16 rows at a time, then the remainder: the workspace holds either plan's partials
+  return counters_bytes(n_total) + gemv_partial_bytes(rows, k, n_total, K) + gemv_pre_bytes(rows, k, n_total);
 }
 
 extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards,
