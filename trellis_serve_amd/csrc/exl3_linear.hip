@@ -41,20 +41,20 @@ __device__ __forceinline__ int find_shard(const ShardArgs& sa, int blk) {
 }
 
 // ---- input rotation of 4 values: lane t of a 32-lane group holds block positions 4t..4t+3 --------------------
+// from the raw 8 bytes of x (fp16 or bf16) and of suh at those positions
 template <bool X_BF16>
-__device__ __forceinline__ void had_in_4(const void* x_row, const uint16_t* __restrict__ suh, int kk, _Float16 h[4]) {
+__device__ __forceinline__ void had_in_raw(uint2_t raw, uint2_t suraw, _Float16 h[4]) {
   _Float16 v[4];
   if constexpr (X_BF16) {
-    const uint2_t raw = *reinterpret_cast<const uint2_t*>(static_cast<const uint16_t*>(x_row) + kk);
     v[0] = (_Float16)bf16_to_f32((uint16_t)(raw.x & 0xFFFF));
     v[1] = (_Float16)bf16_to_f32((uint16_t)(raw.x >> 16));
     v[2] = (_Float16)bf16_to_f32((uint16_t)(raw.y & 0xFFFF));
     v[3] = (_Float16)bf16_to_f32((uint16_t)(raw.y >> 16));
   } else {
-    const half4_t raw = *reinterpret_cast<const half4_t*>(static_cast<const uint16_t*>(x_row) + kk);
-    v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+    const half4_t hv = __builtin_bit_cast(half4_t, raw);
+    v[0] = hv.x; v[1] = hv.y; v[2] = hv.z; v[3] = hv.w;
   }
-  const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
+  const half4_t su = __builtin_bit_cast(half4_t, suraw);
   float f0 = (float)(_Float16)(v[0] * su.x), f1 = (float)(_Float16)(v[1] * su.y);
   float f2 = (float)(_Float16)(v[2] * su.z), f3 = (float)(_Float16)(v[3] * su.w);
   had128_x4(f0, f1, f2, f3);
@@ -62,6 +62,12 @@ __device__ __forceinline__ void had_in_4(const void* x_row, const uint16_t* __re
   h[1] = had_scale_f16(f1);
   h[2] = had_scale_f16(f2);
   h[3] = had_scale_f16(f3);
+}
+
+template <bool X_BF16>
+__device__ __forceinline__ void had_in_4(const void* x_row, const uint16_t* __restrict__ suh, int kk, _Float16 h[4]) {
+  had_in_raw<X_BF16>(*reinterpret_cast<const uint2_t*>(static_cast<const uint16_t*>(x_row) + kk),
+                     *reinterpret_cast<const uint2_t*>(suh + kk), h);
 }
 
 // output rotation of 4 fp16 values (lane t of a 32-lane group: block positions 4t..4t+3), then * svh
@@ -212,16 +218,31 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
   const int tn = sa.tn[s];
+  // prologue: activations of the split, rotated (or as given), into LDS; blocks past the split's end are zero.  One
+  // (row, block) unit per half-wave.  When every half-wave has at most one unit, its activation loads are issued
+  // before the trellis loads: loads complete in issue order, so the rotation then waits only for its own data and
+  // runs while the trellis blocks are in flight.
+  const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
+  const bool single = !PRE && M * NB <= 2 * kGemvWaves;
+  uint2_t xv = uint2_t{0u, 0u}, sv = uint2_t{0u, 0u};
+  if constexpr (!PRE) {
+    const int m = hw / NB, b = hw - m * NB;
+    if (single && hw < M * NB && b < nb) {
+      const int kk = (kb0 + b) * 128 + 4 * t;
+      xv = *reinterpret_cast<const uint2_t*>(static_cast<const uint16_t*>(x) + (size_t)m * k + kk);
+      if constexpr (ROTATE) sv = *reinterpret_cast<const uint2_t*>(sa.suh[s] + kk);
+    }
+  }
+  __asm__ volatile("" ::: "memory");  // keep the activation loads ahead of the trellis loads
+
   Stream stream;
   stream.init(sa.trellis[s], (k >> 4) * tn * 32 * K, tn, (blk - sa.blk0[s]) * kGemvWaves + w, kb0, nb,
               lds + gemv_a_bytes(M, NT) + w * Stream::LDS_BYTES, l);
   stream.start();
 
-  // prologue: activations of the split, rotated (or as given), into LDS; blocks past the split's end are zero
   if constexpr (PRE) {
-    // one (row, block) unit per half-wave, 8 bytes per lane; all loads of the half-wave issued before the stores
+    // prepared rows: 8-byte copies, all loads of the half-wave issued before the stores
     constexpr int IT = kGemvRows * NB / (2 * kGemvWaves);
-    const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
     const uint16_t* pre = static_cast<const uint16_t*>(x) + (size_t)s * pre_rows * k;
     uint2_t v[IT];
 #pragma unroll
@@ -237,8 +258,25 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       const int m = u / NB, b = u - m * NB;
       if (u < M * NB) *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
     }
+  } else if (single) {
+    if (hw < M * NB) {
+      const int m = hw / NB, b = hw - m * NB;
+      _Float16 h[4] = {0, 0, 0, 0};
+      if (b < nb) {
+        if constexpr (ROTATE) {
+          if (x_bf16)
+            had_in_raw<true>(xv, sv, h);
+          else
+            had_in_raw<false>(xv, sv, h);
+        } else {
+          const half4_t v = __builtin_bit_cast(half4_t, xv);
+          h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
+    }
   } else {
-    const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
     for (int u = hw; u < M * NB; u += 2 * kGemvWaves) {
       const int m = u / NB, b = u - m * NB;
       const int kk = (kb0 + b) * 128 + 4 * t;
@@ -344,11 +382,13 @@ static int gemv_target_wgs() {
   return v;
 }
 
-static GemvPlan gemv_plan(int k, int n_total, int M, int K) {
+// pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there
+static GemvPlan gemv_plan(int k, int n_total, int M, int K, bool pre = false) {
   const int kb = k / 128, nblk = n_total / 128;
   int nt = 16;
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
+    if (pre && cand > 32) continue;
     if ((size_t)nblk * splits >= (size_t)gemv_target_wgs() && gemv_lds_bytes(M, cand, K) <= kGemvMaxLds) {
       nt = cand;
       break;
@@ -423,7 +463,7 @@ static size_t gemv_partial_bytes(int rows, int k, int n_total, int K) {
   size_t need = 0;
   for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
     if (M == 0) continue;
-    const GemvPlan pl = gemv_plan(k, n_total, M, K);
+    const GemvPlan pl = gemv_plan(k, n_total, M, K, gemv_pre(rows, k, n_total));
     need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
   }
   return (need + 255) & ~(size_t)255;
@@ -449,15 +489,16 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
   }
   for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
     const int M = std::min(kGemvRows, rows - r0);
-    const GemvPlan pl = gemv_plan(k, n_total, M, K);
+    const GemvPlan pl = gemv_plan(k, n_total, M, K, pre);
     const dim3 grid(n_total / 128, pl.splits);
     const void* xr = static_cast<const uint8_t*>(pre ? (const void*)xh : x) + (size_t)r0 * k * 2;
     void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
     bool ok = false;
 #define EXL3_GEMV_LAUNCH(NTV)                                                                                        \
   if (pl.nt == NTV) {                                                                                                \
-    if (pre)                                                                                                         \
-      ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, NTV, true><<<grid, kGemvThreads, pl.lds, st>>>(    \
+    if (pre) /* the plan gives at most 32 with prepared rows */                                                      \
+      ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, (NTV > 32 ? 32 : NTV), true><<<grid, kGemvThreads,  \
+                                                                                             pl.lds, st>>>(          \
           sa, xr, 0, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows)));                          \
     else if (rotate)                                                                                                 \
       ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, NTV><<<grid, kGemvThreads, pl.lds, st>>>(           \
