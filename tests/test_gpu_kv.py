@@ -137,3 +137,22 @@ def test_kv_decode_page_order_and_padding_invariance():
     assert not first[1].any() and not second[1].any()
     for _ in range(3):
         assert torch.equal(_run(q, kc, vc, ks, vs, table, lens, 8, 0.08), first)
+
+
+def test_kv_decode_shapes_on_one_workspace_and_repeatable():
+    """Calls of different batch / head / length shapes on one workspace, each against the closed form, a
+    zero-length sequence in the batch (its rows are zero), and repeated calls bit-identical."""
+    from trellis_serve_amd import ops
+    ops._kv_ws.clear()
+    sm = D ** -0.5
+    for seed, lens, Hq, Hkv, bits in ((81, [4096, 0, 700], 40, 8, 8), (82, [33], 8, 2, 4), (83, [1500, 2049], 16, 4, 8)):
+        q, kc, vc, ks, vs, table = _case(seed, lens, Hq, Hkv, bits)
+        first = _run(q, kc, vc, ks, vs, table, lens, bits, sm)
+        live = [b for b, L in enumerate(lens) if L > 0]
+        ref = orc.kv_decode_attention(q[live], kc, vc, ks, vs, table[live], np.asarray(lens, np.int32)[live], bits, sm)
+        y = first.cpu().numpy()
+        nrel, mrel = _errs(y[live], ref)
+        assert nrel <= 2e-3 and mrel <= 2e-3, (lens, nrel, mrel)
+        assert all((y[b] == 0).all() for b, L in enumerate(lens) if L == 0)
+        for _ in range(3):
+            assert torch.equal(_run(q, kc, vc, ks, vs, table, lens, bits, sm), first)

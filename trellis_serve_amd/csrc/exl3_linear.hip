@@ -201,8 +201,8 @@ __host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K) {
 // staged by plain 8-byte copies; else x is the input rows, rotated here (ROTATE) or taken as given
 template <int K, int CB, bool ROTATE, int NT, bool PRE = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
-                                                             int M, int k, int splits, float* __restrict__ partial,
-                                                             int* __restrict__ counters, void* __restrict__ y,
+                                                             int M, int k, int splits, float* partial,
+                                                             int* counters, void* __restrict__ y,
                                                              int y_bf16, int n_total, int pre_rows = 0) {
   typedef TileStream<K, CB, NT> Stream;
   constexpr int NB = Stream::NB;

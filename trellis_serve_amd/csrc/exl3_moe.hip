@@ -169,8 +169,8 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(MoeArgs a, const void* __
 template <int K, int CB, int PHASE, int P, bool PRE, int NT>
 __global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
                                                                 uint16_t* __restrict__ gu, uint16_t* __restrict__ dn,
-                                                                float* __restrict__ partial,
-                                                                int* __restrict__ counters, int splits, int chunks) {
+                                                                float* partial,
+                                                                int* counters, int splits, int chunks) {
   typedef TileStream<K, CB, NT> Stream;
   constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
