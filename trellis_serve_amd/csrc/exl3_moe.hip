@@ -165,9 +165,12 @@ __global__ __launch_bounds__(256) void moe_prep_kernel(MoeArgs a, const void* __
   *reinterpret_cast<half2_t*>(row + a_slot(b * 128 + 4 * t + 2, 0, 0)) = half2_t{h[2], h[3]};
 }
 
-// PRE: activations copied from the prep launches' rows (routed mode); else computed here (slot mode, one row)
+// PRE: activations copied from the prep launches' rows (routed mode); else computed here (slot mode, one row).
+// The P = 2 copy-staging kernel is held to 64 VGPRs (8 waves per SIMD, 4 workgroups per CU instead of 3 at its
+// natural 80): it spills 8 bytes (K = 3) and ran 218 -> 192 us at 256 tokens.  P = 4 spills ~100 bytes at the next
+// step down and keeps its 128.
 template <int K, int CB, int PHASE, int P, bool PRE, int NT>
-__global__ __launch_bounds__(kMoeThreads) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
+__global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
                                                                 uint16_t* __restrict__ gu, uint16_t* __restrict__ dn,
                                                                 float* partial,
                                                                 int* counters, int splits, int chunks) {
