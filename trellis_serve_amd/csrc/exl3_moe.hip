@@ -10,21 +10,22 @@
 //
 // Launches (the reference uses five plus an align launch):
 //   single token (slot mode): moe_gemv_kernel<PHASE 0> -> moe_gemv_kernel<PHASE 1> -> moe_combine_kernel; grid row =
-//                      slot, its expert read from topk_ids, the rotations computed inside the expert workgroups.
-//   several tokens: moe_route_kernel -> moe_prep_kernel<0> -> moe_gemv_kernel<PHASE 0> -> moe_prep_kernel<1> ->
-//                      moe_gemv_kernel<PHASE 1> -> moe_combine_kernel; grid row = active expert, the rotated inputs
-//                      written once per slot by the prep launches and copied by the expert workgroups.
-//   moe_route_kernel   one workgroup: per-expert slot counts and lists (LDS atomics), the active experts in
-//                      ascending order.  The order of slots inside an expert's list does not change any result: the
-//                      rows of an MFMA are independent and the combine sums in slot order.
-//   moe_prep_kernel    rotated gate/up inputs fp16(Had(x[token] * suh)) per (slot, shard), then the down inputs
-//                      fp16(Had(fp16(silu(g) * u) * suh_down)) per slot (the reference's moe_had_in and
-//                      moe_glu_had_in launches).
+//                      slot, its expert read from topk_ids; the gate/up reducers write fp16 g|u rows and the down
+//                      workgroups compute the GLU and the input rotations in their prologues.
+//   several tokens: moe_route_prep_kernel -> moe_gemv_kernel<PHASE 0> -> moe_gemv_kernel<PHASE 1> ->
+//                      moe_combine_kernel; grid row = active expert.
+//   moe_route_prep_kernel  the rotated gate/up inputs fp16(Had(x[token] * suh)) per (slot, shard), written once
+//                      (the reference's moe_had_in); its last workgroup routes: per-expert slot counts and lists (LDS
+//                      atomics), the active experts in ascending order.  The order of slots inside an expert's list
+//                      does not change any result: the rows of an MFMA are independent and the combine sums in slot
+//                      order.
 //   moe_gemv_kernel<PHASE 0>  grid (2I/128 column blocks, experts or slots, k-splits): gate/up of every active expert
 //                      for all its slots on the dense GEMV's streaming core (TileStream); up to 16 P slots share each
-//                      decoded tile (P 16-row MFMAs); split-K reduce + output rotation * svh by the last split, fp16
-//                      g|u rows.
-//   moe_gemv_kernel<PHASE 1>  the same for down.
+//                      decoded tile (P 16-row MFMAs).  The gate and up blocks of the same 128 columns count on one
+//                      counter; the last of their splits sums both, applies the output rotations * svh (fp16 g, u),
+//                      then a = fp16(silu(g) * u) (fp32 SiLU), * suh_down and its rotation -- the down inputs of those
+//                      128 positions (the reference's moe_glu_had_in launch, folded in).
+//   moe_gemv_kernel<PHASE 1>  the same for down, staging the prepared down inputs; fp16 d rows.
 //   moe_combine_kernel weighted fp32 sum over the token's slots.
 #include <stdlib.h>
 
@@ -51,44 +52,12 @@ struct MoeArgs {
   const int* lists;        // [E][slots]
   const int* topk_ids;     // [slots]: read directly in slot mode and by the prep launches
   int slot_mode;           // 1: one workgroup row per slot, no routing launch (a single token: its top-k experts)
-  // rotated activations written once per slot by moe_prep_kernel (routed mode): gate/up inputs [2][slots][H], down
-  // inputs [slots][I], each 128-block in the staging order of a_slot
+  // rotated activations written once per slot, each 128-block in the staging order of a_slot: gate/up inputs
+  // [2][slots][H] (moe_route_prep_kernel, several tokens), down inputs [slots][I] (the gate/up reducer, always)
   const uint16_t* pre_in;
   const uint16_t* pre_dn;
 };
 
-
-__global__ __launch_bounds__(1024) void moe_route_kernel(const int* __restrict__ topk_ids, int slots, int E,
-                                                         int* __restrict__ counts, int* __restrict__ n_active,
-                                                         int* __restrict__ active, int* __restrict__ lists) {
-  __shared__ int cnt[1024];
-  __shared__ int scan[1024];
-  const int tid = threadIdx.x;
-  cnt[tid] = 0;
-  __syncthreads();
-  for (int s = tid; s < slots; s += 1024) {
-    const int e = topk_ids[s];
-    if (e >= 0 && e < E) {
-      const int pos = atomicAdd(&cnt[e], 1);
-      lists[(size_t)e * slots + pos] = s;
-    }
-  }
-  __syncthreads();
-  const int flag = tid < E && cnt[tid] > 0;
-  scan[tid] = flag;
-  __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scan
-    const int v = tid >= d ? scan[tid - d] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
-  }
-  if (tid < E) {
-    counts[tid] = cnt[tid];
-    if (flag) active[scan[tid] - 1] = tid;
-  }
-  if (tid == 1023) *n_active = scan[1023];
-}
 
 // LDS: staged activations [16 P rows][NT*16 + 4 halves], then per wave the stream stages; the epilogue reduce reuses
 // it.  P groups of 16 slots share each decoded tile.
@@ -103,75 +72,132 @@ static_assert(moe_lds_bytes<8, 4, 16>() <= 160 * 1024, "MoE LDS must fit a CU");
 
 __device__ __forceinline__ float silu32(float v) { return v / (1.0f + __expf(-v)); }
 
-// The rotated fp16 activations at positions kk .. kk+3 (kk = 128 b + 4 t, lane t of a half-wave) of one slot's input:
-// gate/up (PHASE 0): fp16(x[token] * suh) rotated; down (PHASE 1): a = fp16(silu(g) * u) (fp32 SiLU,
-// exl3_marlin_moe.cu:228-258), * suh, rotated.  One 128-block per half-wave (had128_x4 spans 32 lanes).
-template <int PHASE>
-__device__ __forceinline__ void moe_act4(const MoeArgs& a, const void* x, int x_bf16, const uint16_t* gu,
-                                         const uint16_t* suh, int slot, int kk, _Float16 h[4]) {
-  float f[4];
-  if constexpr (PHASE == 0) {
-    const uint16_t* xr = static_cast<const uint16_t*>(x) + (size_t)(slot / a.top_k) * a.H + kk;
-    _Float16 v[4];
-    if (x_bf16) {
-      const uint2_t raw = *reinterpret_cast<const uint2_t*>(xr);
-      v[0] = (_Float16)bf16_to_f32((uint16_t)(raw.x & 0xFFFF));
-      v[1] = (_Float16)bf16_to_f32((uint16_t)(raw.x >> 16));
-      v[2] = (_Float16)bf16_to_f32((uint16_t)(raw.y & 0xFFFF));
-      v[3] = (_Float16)bf16_to_f32((uint16_t)(raw.y >> 16));
-    } else {
-      const half4_t raw = *reinterpret_cast<const half4_t*>(xr);
-      v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
-    }
-    const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
-    f[0] = (float)(_Float16)(v[0] * su.x); f[1] = (float)(_Float16)(v[1] * su.y);
-    f[2] = (float)(_Float16)(v[2] * su.z); f[3] = (float)(_Float16)(v[3] * su.w);
+// The rotated fp16 gate/up inputs fp16(Had(x[token] * suh)) at positions kk .. kk+3 (kk = 128 b + 4 t, lane t of a
+// half-wave); one 128-block per half-wave (had128_x4 spans 32 lanes).
+__device__ __forceinline__ void moe_in4(const MoeArgs& a, const void* x, int x_bf16, const uint16_t* suh, int slot,
+                                        int kk, _Float16 h[4]) {
+  const uint16_t* xr = static_cast<const uint16_t*>(x) + (size_t)(slot / a.top_k) * a.H + kk;
+  _Float16 v[4];
+  if (x_bf16) {
+    const uint2_t raw = *reinterpret_cast<const uint2_t*>(xr);
+    v[0] = (_Float16)bf16_to_f32((uint16_t)(raw.x & 0xFFFF));
+    v[1] = (_Float16)bf16_to_f32((uint16_t)(raw.x >> 16));
+    v[2] = (_Float16)bf16_to_f32((uint16_t)(raw.y & 0xFFFF));
+    v[3] = (_Float16)bf16_to_f32((uint16_t)(raw.y >> 16));
   } else {
-    const half4_t gv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + kk);
-    const half4_t uv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + a.I + kk);
-    const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
-    f[0] = (float)(f16_of_f32(silu32((float)gv.x) * (float)uv.x) * su.x);
-    f[1] = (float)(f16_of_f32(silu32((float)gv.y) * (float)uv.y) * su.y);
-    f[2] = (float)(f16_of_f32(silu32((float)gv.z) * (float)uv.z) * su.z);
-    f[3] = (float)(f16_of_f32(silu32((float)gv.w) * (float)uv.w) * su.w);
+    const half4_t raw = *reinterpret_cast<const half4_t*>(xr);
+    v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
   }
+  const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
+  float f[4];
+  f[0] = (float)(_Float16)(v[0] * su.x); f[1] = (float)(_Float16)(v[1] * su.y);
+  f[2] = (float)(_Float16)(v[2] * su.z); f[3] = (float)(_Float16)(v[3] * su.w);
   had128_x4(f[0], f[1], f[2], f[3]);
 #pragma unroll
   for (int i = 0; i < 4; i++) h[i] = had_scale_f16(f[i]);
 }
 
-// moe_prep_kernel<PHASE>: the rotated inputs of every routed slot, once (the reference's moe_had_in /
-// moe_glu_had_in launches, exl3_marlin_moe.cu:376-452): one half-wave per (slot, shard, 128-block); rows of
-// unrouted slots are left alone (never read).  Stored in the a_slot order so the GEMV stages them by plain copies.
-template <int PHASE>
-__global__ __launch_bounds__(256) void moe_prep_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
-                                                       const uint16_t* __restrict__ gu, uint16_t* __restrict__ pre) {
-  const int k = PHASE ? a.I : a.H;
-  const int kblocks = k >> 7, nsh = PHASE ? 1 : 2;
-  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (unit >= a.slots * nsh * kblocks) return;
-  const int t = threadIdx.x & 31;
-  const int b = unit % kblocks, rest = unit / kblocks;
-  const int sh = rest % nsh, slot = rest / nsh;
-  const int e = a.topk_ids[slot];
-  if (e < 0 || e >= a.E) return;
-  const uint16_t* suh = a.suh[PHASE ? 2 : sh] + (size_t)e * k;
-  _Float16 h[4];
-  moe_act4<PHASE>(a, x, x_bf16, gu, suh, slot, b * 128 + 4 * t, h);
-  // positions 4t, 4t+1 and 4t+2, 4t+3 land on adjacent staging slots: two 4-byte stores
-  _Float16* row = reinterpret_cast<_Float16*>(pre) + ((size_t)sh * a.slots + slot) * k;
-  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-  *reinterpret_cast<half2_t*>(row + a_slot(b * 128 + 4 * t, 0, 0)) = half2_t{h[0], h[1]};
-  *reinterpret_cast<half2_t*>(row + a_slot(b * 128 + 4 * t + 2, 0, 0)) = half2_t{h[2], h[3]};
+// The rotated down inputs at positions kk .. kk+3 from the fp16 g|u row of a slot: a = fp16(silu(g) * u) in fp32
+// (exl3_marlin_moe.cu:228-258), * suh_down, rotated (single-token path: computed in the down workgroups' prologue)
+__device__ __forceinline__ void moe_glu4(const MoeArgs& a, const uint16_t* gu, const uint16_t* suh, int slot, int kk,
+                                         _Float16 h[4]) {
+  const half4_t gv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + kk);
+  const half4_t uv = *reinterpret_cast<const half4_t*>(gu + (size_t)slot * 2 * a.I + a.I + kk);
+  const half4_t su = *reinterpret_cast<const half4_t*>(suh + kk);
+  float f[4];
+  f[0] = (float)(f16_of_f32(silu32((float)gv.x) * (float)uv.x) * su.x);
+  f[1] = (float)(f16_of_f32(silu32((float)gv.y) * (float)uv.y) * su.y);
+  f[2] = (float)(f16_of_f32(silu32((float)gv.z) * (float)uv.z) * su.z);
+  f[3] = (float)(f16_of_f32(silu32((float)gv.w) * (float)uv.w) * su.w);
+  had128_x4(f[0], f[1], f[2], f[3]);
+#pragma unroll
+  for (int i = 0; i < 4; i++) h[i] = had_scale_f16(f[i]);
 }
 
-// PRE: activations copied from the prep launches' rows (routed mode); else computed here (slot mode, one row).
+// 4 fp16 values into a staging-order row at positions p .. p+3 (p = 4 t): positions 4t, 4t+1 and 4t+2, 4t+3 land on
+// adjacent staging slots, two 4-byte stores
+__device__ __forceinline__ void store_staged4(_Float16* row, int p, const _Float16 h[4]) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<half2_t*>(row + a_slot(p, 0, 0)) = half2_t{h[0], h[1]};
+  *reinterpret_cast<half2_t*>(row + a_slot(p + 2, 0, 0)) = half2_t{h[2], h[3]};
+}
+
+// Routing by one 256-thread workgroup: per-expert slot counts and lists (LDS atomics; ids outside [0, E) skipped),
+// the active experts in ascending order (each thread scans 4 experts, then a workgroup scan of the 256 sums).
+__device__ void moe_route_block(const int* __restrict__ topk_ids, int slots, int E, int* __restrict__ counts,
+                                int* __restrict__ n_active, int* __restrict__ active, int* __restrict__ lists) {
+  __shared__ int cnt[1024];
+  __shared__ int part[256];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < 1024; e += 256) cnt[e] = 0;
+  __syncthreads();
+  for (int s = tid; s < slots; s += 256) {
+    const int e = topk_ids[s];
+    if (e >= 0 && e < E) lists[(size_t)e * slots + atomicAdd(&cnt[e], 1)] = s;
+  }
+  __syncthreads();
+  bool f[4];
+  int loc = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int e = 4 * tid + i;
+    f[i] = e < E && cnt[e] > 0;
+    loc += f[i];
+  }
+  part[tid] = loc;
+  __syncthreads();
+  for (int d = 1; d < 256; d <<= 1) {  // inclusive Hillis-Steele scan
+    const int v = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int base = part[tid] - loc;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int e = 4 * tid + i;
+    if (e < E) {
+      counts[e] = cnt[e];
+      if (f[i]) active[base++] = e;
+    }
+  }
+  if (tid == 255) *n_active = part[255];
+}
+
+// moe_route_prep_kernel: workgroups 0 .. gridDim.x - 2 write the rotated gate/up inputs of every routed slot, one
+// half-wave per (slot, shard, 128-block) (rows of unrouted slots are left alone, never read); the last workgroup
+// routes.  One launch for both: neither needs the other.
+__global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
+                                                             uint16_t* __restrict__ pre, int* __restrict__ counts,
+                                                             int* __restrict__ n_active, int* __restrict__ active,
+                                                             int* __restrict__ lists) {
+  if (blockIdx.x == gridDim.x - 1) {
+    moe_route_block(a.topk_ids, a.slots, a.E, counts, n_active, active, lists);
+    return;
+  }
+  const int kblocks = a.H >> 7;
+  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
+  if (unit >= a.slots * 2 * kblocks) return;
+  const int t = threadIdx.x & 31;
+  const int b = unit % kblocks, rest = unit / kblocks;
+  const int sh = rest & 1, slot = rest >> 1;
+  const int e = a.topk_ids[slot];
+  if (e < 0 || e >= a.E) return;
+  _Float16 h[4];
+  moe_in4(a, x, x_bf16, a.suh[sh] + (size_t)e * a.H, slot, b * 128 + 4 * t, h);
+  store_staged4(reinterpret_cast<_Float16*>(pre) + ((size_t)sh * a.slots + slot) * a.H, b * 128 + 4 * t, h);
+}
+
+// PRE: activations copied from prepared rows (gate/up with several tokens; down always); else the gate/up input
+// rotation is computed here (slot mode, one row).
 // The P = 2 copy-staging kernel is held to 64 VGPRs (8 waves per SIMD, 4 workgroups per CU instead of 3 at its
 // natural 80): it spills 8 bytes (K = 3) and ran 218 -> 192 us at 256 tokens.  P = 4 spills ~100 bytes at the next
 // step down and keeps its 128.
 template <int K, int CB, int PHASE, int P, bool PRE, int NT>
 __global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
-                                                                uint16_t* __restrict__ gu, uint16_t* __restrict__ dn,
+                                                                uint16_t* __restrict__ gu,
+                                                                uint16_t* __restrict__ pre_dn_out,
+                                                                uint16_t* __restrict__ dn,
                                                                 float* partial,
                                                                 int* counters, int splits, int chunks) {
   typedef TileStream<K, CB, NT> Stream;
@@ -256,7 +282,12 @@ __global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv
         for (int u = hw; u < M * NB; u += 2 * kMoeWaves) {
           const int m = u / NB, b = u - m * NB;
           _Float16 h[4] = {0, 0, 0, 0};
-          if (b < nb) moe_act4<PHASE>(a, x, x_bf16, gu, suh, slot_at(c0 + m), (kb0 + b) * 128 + 4 * t, h);
+          if (b < nb) {
+            if constexpr (PHASE == 0)
+              moe_in4(a, x, x_bf16, suh, slot_at(c0 + m), (kb0 + b) * 128 + 4 * t, h);
+            else
+              moe_glu4(a, gu, suh, slot_at(c0 + m), (kb0 + b) * 128 + 4 * t, h);
+          }
 #pragma unroll
           for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
         }
@@ -279,47 +310,89 @@ __global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv
                              __HIP_MEMORY_SCOPE_AGENT);
       }
   }
+  // arrivals: the k-splits of this column block; gate/up with several tokens (GLU) -- the k-splits of the gate block
+  // and of the up block of the same 128 columns, on one counter
+  constexpr bool GLU = PHASE == 0 && PRE;
+  const int ctr = GLU ? ctr_row * (a.I / 128) + cbl : ctr_row * (n_out / 128) + cb;
+  const int arrivals = GLU ? 2 * splits : splits;
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&counters[ctr_row * (n_out / 128) + cb], 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = prev == splits - 1;
+    const int prev = __hip_atomic_fetch_add(&counters[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = prev == arrivals - 1;
   }
   __syncthreads();
   if (!last_flag) return;
 
-  // last split: every slot's 128 columns, splits summed in order, one rounding, output rotation * svh
-  uint16_t* out = PHASE ? dn : gu;
-  const int col = cb * 128 + 4 * t;
-  for (int m = hw; m < n_e; m += 2 * kMoeWaves) {
-    const int slot = slot_at(m);
+  // last arrival: every slot's 128 columns (one slot per half-wave, 4 columns per lane), splits summed in order, one
+  // rounding, output rotation * svh
+  // the splits' loads go out 4 at a time (8-byte device-scope loads; a split past the end reads split 0 again and
+  // adds nothing), then are summed in split order
+  auto finish = [&](int slot, int pcol, const uint16_t* svh4, _Float16 o[4]) {
     float4_t s4 = {0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < splits; p++) {
-      const float* src = partial + ((size_t)p * a.slots + slot) * n_out + col;
-      float4_t v;
-      v.x = __hip_atomic_load(src + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v.y = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v.z = __hip_atomic_load(src + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v.w = __hip_atomic_load(src + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s4 += v;
+    for (int p0 = 0; p0 < splits; p0 += 4) {
+      float4_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int pp = p0 + i < splits ? p0 + i : 0;
+        const uint64_t* src =
+            reinterpret_cast<const uint64_t*>(partial + ((size_t)pp * a.slots + slot) * n_out + pcol);
+        const uint64_t lo = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t hi = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[i] = float4_t{__builtin_bit_cast(float, (uint32_t)lo), __builtin_bit_cast(float, (uint32_t)(lo >> 32)),
+                        __builtin_bit_cast(float, (uint32_t)hi), __builtin_bit_cast(float, (uint32_t)(hi >> 32))};
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (p0 + i < splits) s4 += v[i];
     }
-    _Float16 h[4] = {(_Float16)s4.x, (_Float16)s4.y, (_Float16)s4.z, (_Float16)s4.w};
+    const _Float16 h[4] = {(_Float16)s4.x, (_Float16)s4.y, (_Float16)s4.z, (_Float16)s4.w};
     float f0 = (float)h[0], f1 = (float)h[1], f2 = (float)h[2], f3 = (float)h[3];
     had128_x4(f0, f1, f2, f3);
-    const half4_t sv = *reinterpret_cast<const half4_t*>(svh + cbl * 128 + 4 * t);
-    const half4_t o = {(_Float16)(had_scale_f16(f0) * sv.x), (_Float16)(had_scale_f16(f1) * sv.y),
-                       (_Float16)(had_scale_f16(f2) * sv.z), (_Float16)(had_scale_f16(f3) * sv.w)};
-    *reinterpret_cast<half4_t*>(out + (size_t)slot * n_out + col) = o;
+    const half4_t sv = *reinterpret_cast<const half4_t*>(svh4);
+    o[0] = (_Float16)(had_scale_f16(f0) * sv.x);
+    o[1] = (_Float16)(had_scale_f16(f1) * sv.y);
+    o[2] = (_Float16)(had_scale_f16(f2) * sv.z);
+    o[3] = (_Float16)(had_scale_f16(f3) * sv.w);
+  };
+  if constexpr (GLU) {
+    // g and u of positions kk .. kk+3 of the intermediate, then a = fp16(silu(g) * u) * suh_down rotated: the down
+    // inputs of those positions (exl3_marlin_moe.cu:228-258)
+    const int kk = cbl * 128 + 4 * t;
+    const uint16_t* svg = a.svh[0] + (size_t)e * a.I + kk;
+    const uint16_t* svu = a.svh[1] + (size_t)e * a.I + kk;
+    const half4_t su = *reinterpret_cast<const half4_t*>(a.suh[2] + (size_t)e * a.I + kk);
+    for (int m = hw; m < n_e; m += 2 * kMoeWaves) {
+      const int slot = slot_at(m);
+      _Float16 g[4], u[4];
+      finish(slot, kk, svg, g);
+      finish(slot, a.I + kk, svu, u);
+      float f[4];
+      f[0] = (float)(f16_of_f32(silu32((float)g[0]) * (float)u[0]) * su.x);
+      f[1] = (float)(f16_of_f32(silu32((float)g[1]) * (float)u[1]) * su.y);
+      f[2] = (float)(f16_of_f32(silu32((float)g[2]) * (float)u[2]) * su.z);
+      f[3] = (float)(f16_of_f32(silu32((float)g[3]) * (float)u[3]) * su.w);
+      had128_x4(f[0], f[1], f[2], f[3]);
+      _Float16 h[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) h[i] = had_scale_f16(f[i]);
+      store_staged4(reinterpret_cast<_Float16*>(pre_dn_out) + (size_t)slot * a.I, kk, h);
+    }
+  } else {
+    // fp16 rows: d (down), or g|u (gate/up of a single token: the down prologue applies the GLU, spread over its
+    // workgroups, instead of one half-wave per column block here)
+    uint16_t* out = PHASE ? dn : gu;
+    const int col = cb * 128 + 4 * t;
+    for (int m = hw; m < n_e; m += 2 * kMoeWaves) {
+      const int slot = slot_at(m);
+      _Float16 o[4];
+      finish(slot, col, svh + cbl * 128 + 4 * t, o);
+      *reinterpret_cast<half4_t*>(out + (size_t)slot * n_out + col) = half4_t{o[0], o[1], o[2], o[3]};
+    }
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&counters[ctr_row * (n_out / 128) + cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[ctr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// y[tok, cols] = sum over the token's valid slots, in slot order, of w * dn[slot, cols] in fp32, one rounding
-// (exl3_marlin_moe.cu:262-292).  One half-wave per (token, 128-column block), 4 columns per lane.  The slots are taken
-// 8 at a time: their ids, weights and rows are loaded together (one memory round trip per 8 slots instead of a
-// dependent chain per slot); a skipped slot leaves the sum untouched, exactly as if it were not visited.
 template <bool Y_BF16>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ dn,
                                                           const int* __restrict__ topk_ids,
@@ -414,6 +487,7 @@ static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I, int K) {
   const double high = mean + 2.5 * std::sqrt(mean);
   p.groups = p.slot_mode || high <= 16 ? 1 : high <= 32 ? 2 : 4;
   // the split counters first, in the fixed counter region (zero between calls whatever the shapes)
+  // gate/up counters: per (expert, 128-column block of I) shared by gate and up, or per (slot, block of g|u)
   p.off_cnt_gu = 0;
   p.off_cnt_dn = (size_t)E * (2 * I / 128) * 4;
   size_t o = kCounterBytes;
@@ -421,7 +495,7 @@ static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I, int K) {
   p.off_nactive = o; o = align256(o + 4);
   p.off_active = o; o = align256(o + (size_t)E * 4);
   p.off_lists = o; o = align256(o + (size_t)E * slots * 4);
-  p.off_gu = o; o = align256(o + (size_t)slots * 2 * I * 2);
+  p.off_gu = o; o = align256(o + (p.slot_mode ? (size_t)slots * 2 * I * 2 : 0));
   p.off_dn = o; o = align256(o + (size_t)slots * H * 2);
   p.off_pre_in = o; o = align256(o + (p.slot_mode ? 0 : (size_t)2 * slots * H * 2));
   p.off_pre_dn = o; o = align256(o + (p.slot_mode ? 0 : (size_t)slots * I * 2));
@@ -433,19 +507,20 @@ static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I, int K) {
 
 template <int K, int CB, int PHASE>
 static void launch_moe_gemv(const MoePlan& p, const MoePhase& ph, dim3 grid, const MoeArgs& a, const void* x,
-                            int x_bf16, uint16_t* gu, uint16_t* dn, float* partial, int* counters, hipStream_t st) {
+                            int x_bf16, uint16_t* gu, uint16_t* pre_dn, uint16_t* dn, float* partial, int* counters,
+                            hipStream_t st) {
   const dim3 g3(grid.x, grid.y, ph.splits);
-#define EXL3_MOE_GEMV(P_, PRE_, NT_)                                                                         \
-  moe_gemv_kernel<K, CB, PHASE, P_, PRE_, NT_><<<g3, kMoeThreads, moe_lds_bytes<K, P_, NT_>(), st>>>(        \
-      a, x, x_bf16, gu, dn, partial, counters, ph.splits, ph.chunks)
+#define EXL3_MOE_GEMV(P_, PRE_)                                                                              \
+  moe_gemv_kernel<K, CB, PHASE, P_, PRE_, 16><<<g3, kMoeThreads, moe_lds_bytes<K, P_, 16>(), st>>>(          \
+      a, x, x_bf16, gu, pre_dn, dn, partial, counters, ph.splits, ph.chunks)
   if (p.slot_mode)
-    EXL3_MOE_GEMV(1, false, 16);
+    EXL3_MOE_GEMV(1, false);
   else if (p.groups == 4)
-    EXL3_MOE_GEMV(4, true, 16);
+    EXL3_MOE_GEMV(4, true);
   else if (p.groups == 2)
-    EXL3_MOE_GEMV(2, true, 16);
+    EXL3_MOE_GEMV(2, true);
   else
-    EXL3_MOE_GEMV(1, true, 16);
+    EXL3_MOE_GEMV(1, true);
 #undef EXL3_MOE_GEMV
 }
 
@@ -534,20 +609,16 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   hipStream_t st = as_stream(stream);
 
   if (!a.slot_mode) {
-    moe_route_kernel<<<1, 1024, 0, st>>>(static_cast<const int*>(topk_ids), slots, num_experts, counts, nactive,
-                                         active, lists);
-    EXL3_CHECK_LAUNCH();
-    moe_prep_kernel<0><<<(unsigned)(((size_t)slots * 2 * (hidden / 128) + 7) / 8), 256, 0, st>>>(a, x, x_bf16, gu,
-                                                                                                  pre_in);
+    const unsigned prep_wgs = (unsigned)(((size_t)slots * 2 * (hidden / 128) + 7) / 8);
+    moe_route_prep_kernel<<<prep_wgs + 1, 256, 0, st>>>(a, x, x_bf16, pre_in, counts, nactive, active, lists);
     EXL3_CHECK_LAUNCH();
   }
   const int rows = a.slot_mode ? slots : std::min(num_experts, slots);
   bool ok = EXL3_MOE_DISPATCH(K, codebook, {
-    launch_moe_gemv<kK, kCB, 0>(p, p.gu, dim3(2 * inter / 128, rows), a, x, x_bf16, gu, dn, partial, cnt_gu, st);
-    if (!a.slot_mode)
-      moe_prep_kernel<1><<<(unsigned)(((size_t)slots * (inter / 128) + 7) / 8), 256, 0, st>>>(a, x, x_bf16, gu,
-                                                                                              pre_dn);
-    launch_moe_gemv<kK, kCB, 1>(p, p.dn, dim3(hidden / 128, rows), a, x, x_bf16, gu, dn, partial, cnt_dn, st);
+    launch_moe_gemv<kK, kCB, 0>(p, p.gu, dim3(2 * inter / 128, rows), a, x, x_bf16, gu, pre_dn, dn, partial,
+                                cnt_gu, st);
+    launch_moe_gemv<kK, kCB, 1>(p, p.dn, dim3(hidden / 128, rows), a, x, x_bf16, gu, pre_dn, dn, partial, cnt_dn,
+                                st);
   });
   if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_moe_forward: unsupported K/codebook");
   EXL3_CHECK_LAUNCH();
