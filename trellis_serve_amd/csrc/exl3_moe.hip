@@ -15,7 +15,7 @@
 //   several tokens: moe_route_prep_kernel -> moe_gemv_kernel<PHASE 0> -> moe_gemv_kernel<PHASE 1> ->
 //                      moe_combine_kernel; grid row = active expert.
 //   moe_route_prep_kernel  the rotated gate/up inputs fp16(Had(x[token] * suh)) per (slot, shard), written once
-//                      (the reference's moe_had_in); its last workgroup routes: per-expert slot counts and lists (LDS
+//                      (the reference's moe_had_in); its first workgroup routes: per-expert slot counts and lists (LDS
 //                      atomics), the active experts in ascending order.  The order of slots inside an expert's list
 //                      does not change any result: the rows of an MFMA are independent and the combine sums in slot
 //                      order.
@@ -164,28 +164,38 @@ __device__ void moe_route_block(const int* __restrict__ topk_ids, int slots, int
   if (tid == 255) *n_active = part[255];
 }
 
-// moe_route_prep_kernel: workgroups 0 .. gridDim.x - 2 write the rotated gate/up inputs of every routed slot, one
-// half-wave per (slot, shard, 128-block) (rows of unrouted slots are left alone, never read); the last workgroup
-// routes.  One launch for both: neither needs the other.
+constexpr int kMoePrepUnits = 4;  // 128-blocks per half-wave in moe_route_prep_kernel
+
+// moe_route_prep_kernel: workgroup 0 routes; workgroups 1 .. gridDim.x - 1 write the rotated gate/up inputs of every
+// routed slot, one half-wave per (slot, shard, 4 128-blocks) (rows of unrouted slots are left alone, never read).  One
+// launch for both: neither needs the other.
 __global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
                                                              uint16_t* __restrict__ pre, int* __restrict__ counts,
                                                              int* __restrict__ n_active, int* __restrict__ active,
                                                              int* __restrict__ lists) {
-  if (blockIdx.x == gridDim.x - 1) {
+  if (blockIdx.x == 0) {  // dispatched first: the routing chain is the longest at few tokens
     moe_route_block(a.topk_ids, a.slots, a.E, counts, n_active, active, lists);
     return;
   }
-  const int kblocks = a.H >> 7;
-  const int unit = blockIdx.x * 8 + (threadIdx.x >> 5);
-  if (unit >= a.slots * 2 * kblocks) return;
+  // kMoePrepUnits consecutive 128-blocks of one (slot, shard) row per half-wave: their loads go out together and the
+  // rotations interleave (one block per half-wave was latency-bound: 13 us for 256 tokens)
+  const int kblocks = a.H >> 7, groups = (kblocks + kMoePrepUnits - 1) / kMoePrepUnits;
+  const int u = (blockIdx.x - 1) * 8 + (threadIdx.x >> 5);
   const int t = threadIdx.x & 31;
-  const int b = unit % kblocks, rest = unit / kblocks;
+  const int rest = u / groups, b0 = (u - rest * groups) * kMoePrepUnits;
+  if (rest >= a.slots * 2) return;
   const int sh = rest & 1, slot = rest >> 1;
   const int e = a.topk_ids[slot];
   if (e < 0 || e >= a.E) return;
-  _Float16 h[4];
-  moe_in4(a, x, x_bf16, a.suh[sh] + (size_t)e * a.H, slot, b * 128 + 4 * t, h);
-  store_staged4(reinterpret_cast<_Float16*>(pre) + ((size_t)sh * a.slots + slot) * a.H, b * 128 + 4 * t, h);
+  const uint16_t* suh = a.suh[sh] + (size_t)e * a.H;
+  _Float16* row = reinterpret_cast<_Float16*>(pre) + ((size_t)sh * a.slots + slot) * a.H;
+  _Float16 h[kMoePrepUnits][4];
+#pragma unroll
+  for (int i = 0; i < kMoePrepUnits; i++)
+    if (b0 + i < kblocks) moe_in4(a, x, x_bf16, suh, slot, (b0 + i) * 128 + 4 * t, h[i]);
+#pragma unroll
+  for (int i = 0; i < kMoePrepUnits; i++)
+    if (b0 + i < kblocks) store_staged4(row, (b0 + i) * 128 + 4 * t, h[i]);
 }
 
 // PRE: activations copied from prepared rows (gate/up with several tokens; down always); else the gate/up input
@@ -609,7 +619,8 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   hipStream_t st = as_stream(stream);
 
   if (!a.slot_mode) {
-    const unsigned prep_wgs = (unsigned)(((size_t)slots * 2 * (hidden / 128) + 7) / 8);
+    const unsigned prep_wgs =
+        (unsigned)(((size_t)slots * 2 * ((hidden / 128 + kMoePrepUnits - 1) / kMoePrepUnits) + 7) / 8);
     moe_route_prep_kernel<<<prep_wgs + 1, 256, 0, st>>>(a, x, x_bf16, pre_in, counts, nactive, active, lists);
     EXL3_CHECK_LAUNCH();
   }
