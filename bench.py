@@ -11,9 +11,9 @@ before timing starts; R rotating copies of the layer set (>= 512 MB, twice the 2
 Prints one JSON line: metric/value = algorithmic HBM GB/s of the layer set at M = 1 (trellis + sign vectors +
 activations in/out, BASELINE.md C2 = 128,174,080 B per step), plus the roofline of the dominant kernel (the fused
 decode-GEMV), the CPU baseline (the oracle's decode + matmul on up to 16 host cores, on a bounded sample), the
-M = 4 / 16 rates, and the other configs as reported fields: the single 4096 x 4096 linear of configs[0] (K = 4, 3INST, M = 1), the prefill decode-GEMM
-TFLOPS (configs[2], `decode_gemm_tflops_m2048` is the second half of the metric), the MoE layer and the
-quantized-KV decode attention.  For scale: the warm (single copy) layer-set rate, the trellis-only
+M = 4 / 16 rates, and the other configs as reported fields: the single 4096 x 4096 linear of configs[0] (K = 4,
+3INST, M = 1), the prefill decode-GEMM TFLOPS (configs[2], `decode_gemm_tflops_m2048` is the second half of the
+metric), the MoE layer and the quantized-KV decode attention.  For scale: the warm (single copy) layer-set rate, the trellis-only
 weight-stream rate, hipBLASLt's fp16 8192^3 GEMM, and the reference's prefill design (W decoded to HBM, then the vendor
 GEMM) rebuilt on this box at configs[2] M = 2048.
 """
