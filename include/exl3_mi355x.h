@@ -122,7 +122,8 @@ typedef struct exl3_moe_weights {
   const void* down_svh;     /* fp16 [E][H] */
 } exl3_moe_weights;
 
-/* Workspace bytes of exl3_moe_forward (split counters, routing lists, fp16 g|u and down rows, fp32 partials).  The
+/* Workspace bytes of exl3_moe_forward (split counters, routing lists, fp16 rotated inputs, g|u and down rows, fp32
+ * partials).  The
  * counter region (EXL3_WORKSPACE_COUNTER_BYTES, holding num_experts * (2 inter + hidden) / 128 counters) must be
  * zero before the first use; every call leaves it zero. */
 size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K);
@@ -130,7 +131,8 @@ size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidd
  * linear with its own suh / svh; fp32 combine in slot order; ids outside [0, E) are skipped.  x fp16|bf16 [T, H],
  * topk_ids int32 [T, top_k], topk_weights fp32 [T, top_k], y fp16|bf16 [T, H].  Replaces the five launches of
  * cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294 (moe_had_in, moe_gemm, moe_glu_had_in, moe_gemm,
- * moe_combine; cuda/csrc/exl3_marlin_moe.cu:376-499) and the align step (exl3_marlin_moe.cu:532-594). */
+ * moe_combine; cuda/csrc/exl3_marlin_moe.cu:376-499) and the align step (exl3_marlin_moe.cu:532-594) with four
+ * launches (three for a single token).  Calls that share a workspace must not overlap. */
 int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids, const void* topk_weights,
                      int top_k, int num_experts, int inter, const exl3_moe_weights* weights_host, int K, int codebook,
                      void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);

@@ -211,8 +211,8 @@ def test_moe_full_shape_batched_tokens_match_single_token(coracle):
 
 @pytest.mark.parametrize("T", [3, 20, 40, 300])
 def test_moe_slot_groups_and_passes_match_exact_layer(T):
-    """Several tokens: routing launch, rotated inputs prepared once per slot, up to 16 P slots sharing each decoded
-    tile.  3 / 20 / 40 / 300 tokens over 8 experts run P = 1 / 2 / 4 / 4 groups (40 tokens: one pass of 40 slots per
+    """Several tokens: routing + input rotation launch, up to 16 P slots sharing each decoded tile, the GLU folded into
+    the gate/up reducer.  3 / 20 / 40 / 300 tokens over 8 experts run P = 1 / 2 / 4 / 4 groups (40 tokens: one pass of 40 slots per
     expert in 3 groups; 300 tokens: 300 slots per expert, several passes).  Every token against the exact layer, and
     two tokens against their single-token calls (slot mode: other k-split plan) within 1e-3."""
     from trellis_serve_amd import ops

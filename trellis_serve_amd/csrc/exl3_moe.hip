@@ -50,10 +50,10 @@ struct MoeArgs {
   const int* n_active;     // [1]
   const int* active;       // [E]: active experts, ascending
   const int* lists;        // [E][slots]
-  const int* topk_ids;     // [slots]: read directly in slot mode and by the prep launches
+  const int* topk_ids;     // [slots]: read directly in slot mode and by the route+prep launch
   int slot_mode;           // 1: one workgroup row per slot, no routing launch (a single token: its top-k experts)
   // rotated activations written once per slot, each 128-block in the staging order of a_slot: gate/up inputs
-  // [2][slots][H] (moe_route_prep_kernel, several tokens), down inputs [slots][I] (the gate/up reducer, always)
+  // [2][slots][H] (moe_route_prep_kernel) and down inputs [slots][I] (the gate/up reducer), both for several tokens
   const uint16_t* pre_in;
   const uint16_t* pre_dn;
 };
