@@ -43,6 +43,11 @@ __device__ __forceinline__ _Float16 had_scale_f16(float f) { return f16_of_f32(f
 // 15:14, expcnt 6:4, lgkmcnt 11:8)
 __host__ __device__ constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
+// Workgroup barrier that waits for this wave's LDS accesses only.  __syncthreads() adds a workgroup fence, which
+// makes the compiler wait for every outstanding global load (vmcnt(0)) and would drain loads that are meant to stay
+// in flight across the barrier; LDS data written from loaded values is waited for by its own data dependence.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---- per-lane tile geometry ----------------------------------------------------------------------------------
 struct LaneGeo {
   int dw0, dw1;  // tile dwords holding the lane's bits (dw1 = dw0 + 1, circular)

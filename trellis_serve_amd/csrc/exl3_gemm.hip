@@ -78,10 +78,8 @@ struct GemmPlan {
   int* counters;   // [tail tiles], zero between calls
 };
 
-// Workgroup barrier that waits for this wave's LDS accesses only.  __syncthreads() adds a workgroup fence, which
-// makes the compiler wait for every outstanding load (vmcnt(0)) and would drain the direct-to-LDS pipeline; the
-// direct-to-LDS writes are waited for explicitly (waitcnt_vm) before each barrier instead.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// lds_barrier() (exl3_device.hpp) between k-steps: the direct-to-LDS writes are waited for explicitly (waitcnt_vm)
+// before each barrier.
 
 template <int K>
 __host__ __device__ constexpr int gemm_chunks() { return 4 * 32 * K / 16; }  // 16-byte pieces of a wave's 4 tiles

@@ -192,8 +192,8 @@ constexpr int kWaitVmcnt0 = 0x0F70;      // s_waitcnt vmcnt(0) (expcnt, lgkmcnt 
 // bytes; at least 16 * 128 fp32 for the epilogue reduce
 __host__ __device__ constexpr int gemv_a_bytes(int M, int NT) { return ((M * (NT * 16 + 4) * 2) + 15) & ~15; }
 __host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K) {
-  return gemv_a_bytes(M, NT) + kGemvWaves * 2 * 256 * K > kGemvThreads * 16
-             ? gemv_a_bytes(M, NT) + kGemvWaves * 2 * 256 * K
+  return gemv_a_bytes(M, NT) + kGemvWaves * stream_lds_bytes(K) > kGemvThreads * 16
+             ? gemv_a_bytes(M, NT) + kGemvWaves * stream_lds_bytes(K)
              : kGemvThreads * 16;
 }
 

@@ -59,16 +59,14 @@ struct MoeArgs {
 };
 
 
-// LDS: staged activations [16 P rows][NT*16 + 4 halves], then per wave the stream stages; the epilogue reduce reuses
-// it.  P groups of 16 slots share each decoded tile.
-template <int K, int P, int NT>
+// LDS: staged activations [16 P rows][NT*16 + 4 halves] (two such buffers with prepared rows: chunk c + 1 is staged
+// while chunk c decodes), then per wave the stream stages.  P groups of 16 slots share each decoded tile.
+template <int K, int P, int NT, bool PRE>
 __host__ __device__ constexpr int moe_lds_bytes() {
-  return kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, NT>::LDS_BYTES > kMoeThreads * 16
-             ? kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, NT>::LDS_BYTES
-             : kMoeThreads * 16;
+  return (PRE ? 2 : 1) * kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, NT>::LDS_BYTES;
 }
 
-static_assert(moe_lds_bytes<8, 4, 16>() <= 160 * 1024, "MoE LDS must fit a CU");
+static_assert(moe_lds_bytes<8, 4, 16, true>() <= 160 * 1024, "MoE LDS must fit a CU");
 
 __device__ __forceinline__ float silu32(float v) { return v / (1.0f + __expf(-v)); }
 
@@ -200,11 +198,11 @@ __global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const vo
 
 // PRE: activations copied from prepared rows (gate/up with several tokens; down always); else the gate/up input
 // rotation is computed here (slot mode, one row).
-// The P = 2 copy-staging kernel is held to 64 VGPRs (8 waves per SIMD, 4 workgroups per CU instead of 3 at its
-// natural 80): it spills 8 bytes (K = 3) and ran 218 -> 192 us at 256 tokens.  P = 4 spills ~100 bytes at the next
-// step down and keeps its 128.
+// The prepared-row kernels with P <= 2 and K <= 4 are held to 64 VGPRs (8 waves per SIMD), which they reach without
+// spilling; the others take what they need (P = 4 and K >= 5: 80-130 VGPRs; P = 4 is held to one workgroup per CU by
+// its LDS anyway).
 template <int K, int CB, int PHASE, int P, bool PRE, int NT>
-__global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
+__global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
                                                                 uint16_t* __restrict__ gu,
                                                                 uint16_t* __restrict__ pre_dn_out,
                                                                 uint16_t* __restrict__ dn,
@@ -254,7 +252,7 @@ __global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
   const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
-  uint8_t* stage = lds + kMoeRows * P * mstride * 2 + w * Stream::LDS_BYTES;
+  uint8_t* stage = lds + (PRE ? 2 : 1) * kMoeRows * P * mstride * 2 + w * Stream::LDS_BYTES;
 
   // passes of up to 16 P slots; each decoded tile feeds the pass's `groups` 16-row MFMAs
   for (int c0 = 0; c0 < n_e; c0 += kMoeRows * P) {
@@ -263,32 +261,87 @@ __global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv
     float4_t acc[P];
 #pragma unroll
     for (int p = 0; p < P; p++) acc[p] = float4_t{0.f, 0.f, 0.f, 0.f};
-    for (int ch = 0; ch < chunks; ch++) {
-      const int kb0 = (sp * chunks + ch) * NB;
-      if (kb0 >= kblocks) break;
-      const int nb = min(kblocks, kb0 + NB) - kb0;
-      Stream stream;
-      stream.init(trellis, mat_bytes, tn, cbl * kMoeWaves + w, kb0, nb, stage, l);
-      stream.start();
-      if constexpr (PRE) {
-        // precomputed rows: 128-block copies (8 bytes per lane), all loads of the half-wave issued before the stores
-        constexpr int IT = kMoeRows * P * NB / (2 * kMoeWaves);
-        uint2_t v[IT];
+    if constexpr (PRE) {
+      // prepared rows, chunk after chunk, with the next chunk's rows and trellis blocks in flight while this one
+      // decodes: two streams and two activation buffers alternate (the loop carries no register copies, so the
+      // compiler's in-order load waits stay exact).  Every load is unconditional -- a unit past the pass's rows or
+      // the split's blocks reads out of the buffer's range and gets zeros, a prefetch past the split's last chunk
+      // re-reads that chunk (in range, never used) -- and the slot rows' offsets are read once per pass, so no load
+      // inside the loop waits on an older one.
+      constexpr int IT = kMoeRows * P * NB / (2 * kMoeWaves);
+      static_assert((2 * kMoeWaves) % NB == 0, "a half-wave keeps its block across its units");
+      const int nch = min(chunks, (kblocks + NB - 1) / NB - sp * chunks);  // this split's chunks (>= 1)
+      const uint32_t pre_bytes = (uint32_t)a.slots * (uint32_t)k * 2u;
+      const __amdgpu_buffer_rsrc_t prs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)pre, (short)0, (int)pre_bytes, 0x00020000);
+      const int ub = hw % NB;  // the half-wave's block inside a chunk (the same for all its units)
+      uint32_t rowoff[IT];     // byte offset of each unit's slot row; pre_bytes (out of range) past the pass's rows
+#pragma unroll
+      for (int it = 0; it < IT; it++) {
+        const int m = hw / NB + it * (2 * kMoeWaves / NB);
+        rowoff[it] = m < M ? (uint32_t)slot_at(c0 + m) * (uint32_t)k * 2u : pre_bytes;
+      }
+      auto chunk_kb0 = [&](int ch) { return (sp * chunks + (ch < nch ? ch : nch - 1)) * NB; };
+      auto load_a = [&](int ch, uint2_t (&v)[IT]) {
+        const int kb0 = chunk_kb0(ch);
+        const bool live = ub < min(kblocks, kb0 + NB) - kb0;
+        const uint32_t col = (uint32_t)((kb0 + ub) * 128 + 4 * t) * 2u;
 #pragma unroll
         for (int it = 0; it < IT; it++) {
-          const int u = hw + it * 2 * kMoeWaves;
-          const int m = u / NB, b = u - m * NB;
-          v[it] = uint2_t{0u, 0u};
-          if (u < M * NB && b < nb)
-            v[it] = *reinterpret_cast<const uint2_t*>(pre + (size_t)slot_at(c0 + m) * k + (kb0 + b) * 128 + 4 * t);
+          const uint32_t off = live && rowoff[it] < pre_bytes ? rowoff[it] + col : pre_bytes;
+          v[it] = __builtin_bit_cast(uint2_t, __builtin_amdgcn_raw_buffer_load_b64(prs, off, 0, 0));
         }
+      };
+      // every row of the buffer is written (zeros past the pass's rows), so no store is conditional either
+      auto store_a = [&](_Float16* dst, const uint2_t (&v)[IT]) {
 #pragma unroll
         for (int it = 0; it < IT; it++) {
-          const int u = hw + it * 2 * kMoeWaves;
-          const int m = u / NB, b = u - m * NB;
-          if (u < M * NB) *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
+          const int m = hw / NB + it * (2 * kMoeWaves / NB);
+          *reinterpret_cast<uint2_t*>(dst + m * mstride + ub * 128 + 4 * t) = v[it];
         }
-      } else {
+      };
+      auto start = [&](Stream& st, int ch) {
+        const int kb0 = chunk_kb0(ch);
+        st.init(trellis, mat_bytes, tn, cbl * kMoeWaves + w, kb0, min(kblocks, kb0 + NB) - kb0, stage, l);
+        st.start();
+      };
+      _Float16* xs1 = xs + kMoeRows * P * mstride;
+      // A row of lane group c in group p: 16 p + c (group 0: min(c, M - 1)); rows >= M feed only C rows never stored
+      const half4_t* ap0 = reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j;
+      const half4_t* ap1 = reinterpret_cast<const half4_t*>(xs1 + min(c, M - 1) * mstride) + j;
+      Stream s0, s1;
+      uint2_t v[IT];
+      load_a(0, v);
+      start(s0, 0);
+      store_a(xs, v);
+      lds_barrier();
+      // chunks in pairs, then an odd last one: the loop has no early exit, so every path into its head carries the
+      // same loads in flight (stream 0's) and the compiler's load waits inside stay exact
+      int ch = 0;
+      for (; ch + 2 <= nch; ch += 2) {
+        load_a(ch + 1, v);
+        start(s1, ch + 1);
+        s0.template run_groups<P>(ap0, kMoeRows * mstride / 4, groups, acc);
+        store_a(xs1, v);
+        lds_barrier();  // chunk ch + 1 staged; every wave is done with buffer 0
+        load_a(ch + 2, v);
+        start(s0, ch + 2);
+        s1.template run_groups<P>(ap1, kMoeRows * mstride / 4, groups, acc);
+        store_a(xs, v);
+        lds_barrier();
+      }
+      if (ch < nch) {  // the odd last chunk: staged in buffer 0, its blocks in stream 0
+        s0.template run_groups<P>(ap0, kMoeRows * mstride / 4, groups, acc);
+        lds_barrier();
+      }
+    } else {
+      for (int ch = 0; ch < chunks; ch++) {
+        const int kb0 = (sp * chunks + ch) * NB;
+        if (kb0 >= kblocks) break;
+        const int nb = min(kblocks, kb0 + NB) - kb0;
+        Stream stream;
+        stream.init(trellis, mat_bytes, tn, cbl * kMoeWaves + w, kb0, nb, stage, l);
+        stream.start();
         for (int u = hw; u < M * NB; u += 2 * kMoeWaves) {
           const int m = u / NB, b = u - m * NB;
           _Float16 h[4] = {0, 0, 0, 0};
@@ -301,12 +354,12 @@ __global__ __launch_bounds__(kMoeThreads, (P == 2 && PRE) ? 8 : 1) void moe_gemv
 #pragma unroll
           for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
         }
+        __syncthreads();
+        // A row of lane group c in group p: 16 p + c (group 0: min(c, M - 1)); rows >= M feed only C rows never stored
+        stream.template run_groups<P>(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j,
+                                      kMoeRows * mstride / 4, groups, acc);
+        __syncthreads();  // the next chunk or pass restages LDS
       }
-      __syncthreads();
-      // A row of lane group c in group p: 16 p + c (group 0: min(c, M - 1)); rows >= M feed only C rows never stored
-      stream.template run_groups<P>(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j,
-                                    kMoeRows * mstride / 4, groups, acc);
-      __syncthreads();  // the next chunk or pass restages LDS
     }
     // this split's partial rows, device-coherent (read by the last split, possibly on another XCD)
     float* pdst = partial + (size_t)sp * a.slots * n_out + cb * 128 + w * 16 + c;
@@ -521,7 +574,7 @@ static void launch_moe_gemv(const MoePlan& p, const MoePhase& ph, dim3 grid, con
                             hipStream_t st) {
   const dim3 g3(grid.x, grid.y, ph.splits);
 #define EXL3_MOE_GEMV(P_, PRE_)                                                                              \
-  moe_gemv_kernel<K, CB, PHASE, P_, PRE_, 16><<<g3, kMoeThreads, moe_lds_bytes<K, P_, 16>(), st>>>(          \
+  moe_gemv_kernel<K, CB, PHASE, P_, PRE_, 16><<<g3, kMoeThreads, moe_lds_bytes<K, P_, 16, PRE_>(), st>>>(    \
       a, x, x_bf16, gu, pre_dn, dn, partial, counters, ph.splits, ph.chunks)
   if (p.slot_mode)
     EXL3_MOE_GEMV(1, false);
