@@ -13,9 +13,9 @@
 //      (c, j) of a tile the 4 weights of column c at rows r(j, 0..3); tile row tr of the k-step supplies halves
 //      4tr..4tr+3 of the lane's 8-half B fragment.  A and B then agree on the k order of every MFMA.
 //
-// Tiling: workgroup 256 rows x 128 columns (one output rotation block), 4 waves as 2 x 2, wave tile 128 x 64
-// (8 x 4 MFMA 16x16x32 tiles, 128 fp32 accumulators per lane).  Two workgroups fit a CU (LDS and VGPRs), so
-// 2 x CUs tiles run at once.
+// Tiling: workgroup 256 rows x 256 columns (two output rotation blocks; a shard of an odd number of 128-column blocks
+// ends in a half tile), 8 waves as 2 x 4, wave tile 128 x 64 (8 x 4 MFMA 16x16x32 tiles, 128 fp32 accumulators per
+// lane).  135 KB of LDS: one workgroup per CU, CUs tiles at once.
 //
 // Work decomposition (1-D grid of work items, dispatched in order): tiles are numbered column block fastest, so
 // consecutive workgroups share their A rows in L2.  R x slots tiles (R whole rounds of the machine) are data-parallel
@@ -27,13 +27,13 @@
 // independent of arrival order), then runs the same epilogue as a data-parallel item and resets the counter.
 //
 // Pipeline: direct-to-LDS 16-byte buffer loads (no VGPR staging) into two 3-slot rings, one for A (per k-step each
-// wave loads 4 pieces, one m-block of 64 lanes x 16 B: a lane's 16 bytes land exactly where its MFMA A fragment lives)
-// and one for the trellis bits (each wave loads its 4 tiles of the k-step).  A bundle of loads holds A of step b and
-// the bits of step b+1 and is issued two steps before its A is used, so every load has two steps of flight while the
-// LDS stays under 80 KB (two workgroups per CU).  The compiler does not order LDS-DMA writes before LDS reads, so the
-// waits are explicit (vmcnt), and one barrier per k-step publishes the other waves' pieces and decoded weights.
-// Each k-step runs its 32 MFMAs next to the decode of the following k-step (16 tiles per workgroup, 4 per wave, into
-// a double-buffered fp16 B fragment area), so VALU decode work overlaps matrix work.
+// wave loads 2 pieces, one m-block of 64 lanes x 16 B each: a lane's 16 bytes land exactly where its MFMA A fragment
+// lives) and one for the trellis bits (each wave loads its 4 tiles of the k-step).  A bundle of loads holds A of step
+// b and the bits of step b+1 and is issued two steps before its A is used, so every load has two steps of flight.
+// The compiler does not order LDS-DMA writes before LDS reads, so the waits are explicit (vmcnt), and one barrier per
+// k-step publishes the other waves' pieces and decoded weights.  Each k-step runs its 32 MFMAs per wave next to the
+// decode of the following k-step (32 tiles per workgroup, 4 per wave, into a double-buffered fp16 B fragment area),
+// so VALU decode work overlaps matrix work.
 #include <stdlib.h>
 
 #include <algorithm>
