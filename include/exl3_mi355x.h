@@ -129,8 +129,8 @@ typedef struct exl3_moe_weights {
 size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K);
 /* y[t] = sum_j w[t, j] * down_e(fp16(silu(gate_e(x[t])) * up_e(x[t]))), e = topk_ids[t, j]; every linear is an EXL3
  * linear with its own suh / svh; fp32 combine in slot order; ids outside [0, E) are skipped.  x fp16|bf16 [T, H],
- * topk_ids int32 [T, top_k], topk_weights fp32 [T, top_k], y fp16|bf16 [T, H].  Replaces the five launches of
- * cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294 (moe_had_in, moe_gemm, moe_glu_had_in, moe_gemm,
+ * topk_ids int32 [T, top_k] (top_k <= 64), topk_weights fp32 [T, top_k], y fp16|bf16 [T, H].  Replaces the five
+ * launches of cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294 (moe_had_in, moe_gemm, moe_glu_had_in, moe_gemm,
  * moe_combine; cuda/csrc/exl3_marlin_moe.cu:376-499) and the align step (exl3_marlin_moe.cu:532-594) with four
  * launches (three for a single token).  Calls that share a workspace must not overlap. */
 int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids, const void* topk_weights,

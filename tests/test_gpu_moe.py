@@ -144,6 +144,32 @@ def test_moe_single_token_all_unrouted_is_zero():
     assert (y == 0).all()
 
 
+@pytest.mark.parametrize("top_k", [4, 64])
+def test_moe_single_token_top_k_range_bf16_and_repeat(top_k):
+    """A single token up to the largest top-k (64; one grid row per slot): against the exact layer, bf16 out equal to
+    fp16 out to bf16's half-ulp (one rounding of the same fp32 sum), repeat calls bit-identical, one unrouted slot
+    skipped."""
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(50 + top_k)
+    E, H, I, K = 128, 256, 128, 3
+    ex = _experts(rng, E, H, I, K)
+    st = _stack(ex)
+    x = (rng.standard_normal((1, H)) * 0.5).astype(np.float16)
+    ids = rng.permutation(E)[:top_k].astype(np.int32)[None]
+    ids[0, top_k // 2] = -1
+    w = (rng.random((1, top_k)) / top_k).astype(np.float32)
+    xd, idd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    y = ops.moe_forward(xd, idd, wd, st, 1)
+    nrel, mrel = _errs(y.cpu().numpy(), orc.moe_forward(x, ids, w, ex, K, 1))
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+    yb = ops.moe_forward(xd.bfloat16(), idd, wd, st, 1)
+    assert yb.dtype == torch.bfloat16
+    yh = ops.moe_forward(xd.bfloat16(), idd, wd, st, 1, out=torch.empty((1, H), dtype=torch.float16, device="cuda"))
+    assert ((yb.float() - yh.float()).abs() <= yh.float().abs() * 2.0 ** -8 + 1e-6).all()
+    for _ in range(3):
+        assert torch.equal(ops.moe_forward(xd, idd, wd, st, 1), y)
+
+
 def test_moe_many_slots_use_the_routing_launch():
     """2080 slots over 8 experts (260 per expert: passes of 64 slots, the last one partial); both ends of the token
     range against the exact layer, and a repeat is bit-identical."""

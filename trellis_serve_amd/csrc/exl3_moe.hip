@@ -67,6 +67,7 @@ __host__ __device__ constexpr int moe_lds_bytes() {
 }
 
 static_assert(moe_lds_bytes<8, 4, 16, true>() <= 160 * 1024, "MoE LDS must fit a CU");
+constexpr int kMoeMaxTopK = 64;
 
 __device__ __forceinline__ float silu32(float v) { return v / (1.0f + __expf(-v)); }
 
@@ -617,7 +618,7 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
                                 size_t workspace_bytes, void* stream) {
   EXL3_CHECK_ARG(x && y && topk_ids && topk_weights && w, "exl3_moe_forward: null pointer");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_moe_forward: K = %d / codebook = %d", K, codebook);
-  EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= 64, "exl3_moe_forward: tokens = %d, top_k = %d", tokens, top_k);
+  EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= kMoeMaxTopK, "exl3_moe_forward: tokens = %d, top_k = %d", tokens, top_k);
   EXL3_CHECK_ARG(num_experts >= 1 && num_experts <= 1024, "exl3_moe_forward: num_experts = %d (1..1024)", num_experts);
   EXL3_CHECK_ARG(hidden > 0 && hidden % 128 == 0 && inter > 0 && inter % 128 == 0,
                  "exl3_moe_forward: hidden = %d, inter = %d (multiples of 128)", hidden, inter);
