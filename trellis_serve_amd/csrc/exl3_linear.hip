@@ -334,17 +334,20 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
     const int m = unit >> 5, q = unit & 31;
     const int base = (m * n_total + col_blk + 4 * q) * 4;
     const int pstride = M * n_total * 4;
+    // up to 8 loads in flight per round (only for splits that exist), summed in split order
     float4_t a = {0.f, 0.f, 0.f, 0.f};
-    int p = gq;
-    for (; p + 3 * G < splits; p += 4 * G) {
-      const float4_t v0 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + p * pstride, 0, kCoherentDevice));
-      const float4_t v1 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + (p + G) * pstride, 0, kCoherentDevice));
-      const float4_t v2 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + (p + 2 * G) * pstride, 0, kCoherentDevice));
-      const float4_t v3 = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + (p + 3 * G) * pstride, 0, kCoherentDevice));
-      a += v0; a += v1; a += v2; a += v3;
+    for (int p0 = gq; p0 < splits; p0 += 8 * G) {
+      float4_t v[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        v[i] = p0 + i * G < splits ? __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                      prsrc, base + (p0 + i * G) * pstride, 0,
+                                                                      kCoherentDevice))
+                                   : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (p0 + i * G < splits) a += v[i];
     }
-    for (; p < splits; p += G)
-      a += __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(prsrc, base + p * pstride, 0, kCoherentDevice));
     red[gq * units + unit] = a;
   }
   __syncthreads();
@@ -374,12 +377,14 @@ struct GemvPlan {
   size_t lds;
 };
 
-static int gemv_target_wgs() {
-  static const int v = [] {
+// the workgroup target: 1536 below 8 rows; from 8 rows, where every split's fp32 partial of M rows is written and
+// read again and the last split's reduce reads all of them, half that (measured at 16 rows: down 31.5 -> 29.0 us)
+static int gemv_target_wgs(int M) {
+  static const int env = [] {
     const char* e = getenv("EXL3_GEMV_TARGET_WGS");
-    return e ? std::max(1, atoi(e)) : 1536;
+    return e ? std::max(1, atoi(e)) : 0;
   }();
-  return v;
+  return env ? env : M >= 8 ? 768 : 1536;
 }
 
 // pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there
@@ -389,7 +394,7 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K, bool pre = false) {
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
     if (pre && cand > 32) continue;
-    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs() && gemv_lds_bytes(M, cand, K) <= kGemvMaxLds) {
+    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs(M) && gemv_lds_bytes(M, cand, K) <= kGemvMaxLds) {
       nt = cand;
       break;
     }
