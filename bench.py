@@ -465,7 +465,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--rows", type=int, default=1)
     ap.add_argument("--copies", type=int, default=5, help="rotating copies of the layer set (cold HBM)")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -63,7 +63,7 @@ struct MoeArgs {
 // while chunk c decodes), then per wave the stream stages.  P groups of 16 slots share each decoded tile.
 template <int K, int P, int NT, bool PRE>
 __host__ __device__ constexpr int moe_lds_bytes() {
-  return (PRE ? 2 : 1) * kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * TileStream<K, 0, NT>::LDS_BYTES;
+  return (PRE ? 2 : 1) * kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * stream_lds_bytes(K, PRE);
 }
 
 static_assert(moe_lds_bytes<8, 4, 16, true>() <= 160 * 1024, "MoE LDS must fit a CU");
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
                                                                 uint16_t* __restrict__ dn,
                                                                 float* partial,
                                                                 int* counters, int splits, int chunks) {
-  typedef TileStream<K, CB, NT> Stream;
+  typedef TileStream<K, CB, NT, PRE> Stream;  // the prepared-row chunk pipeline needs every lane loading
   constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;

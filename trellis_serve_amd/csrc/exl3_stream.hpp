@@ -19,17 +19,25 @@ namespace exl3 {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// LDS bytes of one wave's stream: two block stages of one 1 KB gather slot (64 lanes x 16 B) per 64 chunks
-__host__ __device__ constexpr int stream_lds_bytes(int K) { return 2 * ((16 * K + 63) / 64) * 1024; }
+// LDS bytes of one wave's stream: two block stages, each 256 K bytes (the block's data), or, with every lane loading
+// (ALL_LANES), one 1 KB gather slot (64 lanes x 16 B) per 64 chunks
+__host__ __device__ constexpr int stream_lds_bytes(int K, bool all_lanes = false) {
+  return all_lanes ? 2 * ((16 * K + 63) / 64) * 1024 : 2 * 256 * K;
+}
 
-template <int K, int CB, int NT>
+// ALL_LANES: lanes past the last chunk still load -- from beyond the buffer's end, which reads zeros -- and write their
+// stage slot, so that no load or stage write is lane-conditional.  A lane-conditional load is a branch the compiler
+// must assume taken or skipped, which turns its in-order load waits into vmcnt(0) in a loop that keeps loads in
+// flight across iterations (the MoE chunk pipeline); straight-line callers (the dense GEMV) keep the lane mask, which
+// spends fewer address cycles (48 of 64 lanes at K = 3).
+template <int K, int CB, int NT, bool ALL_LANES = false>
 struct TileStream {
   static constexpr int NB = NT / 8;               // 128-row blocks
   static constexpr int CHUNKS = 16 * K;           // 16-byte chunks in the 8 tiles of one block column
   static constexpr int LPB = (CHUNKS + 63) / 64;  // wave-wide gathers per block
-  static constexpr int STAGE = LPB * 1024;        // bytes of one block stage: every lane of every gather writes
-  static constexpr int LDS_BYTES = 2 * STAGE;     // per wave (= stream_lds_bytes(K))
-  static_assert(LDS_BYTES == stream_lds_bytes(K), "stage size");
+  static constexpr int STAGE = ALL_LANES ? LPB * 1024 : 256 * K;  // bytes of one block stage
+  static constexpr int LDS_BYTES = 2 * STAGE;                        // per wave
+  static_assert(LDS_BYTES == stream_lds_bytes(K, ALL_LANES), "stage size");
   // a lane offset past every buffer this stream reads (matrices stay below 2^31 bytes; offset + block offset never
   // wraps 32 bits)
   static constexpr int kOutOfRange = 0x7FFFFFF0;
@@ -37,6 +45,7 @@ struct TileStream {
   __amdgpu_buffer_rsrc_t rsrc;
   int soff0, row_bytes, nb, lane;
   int goff[LPB];
+  bool glive[LPB];
   u32x4_t buf[NB][LPB];
   uint8_t* stage;
   LaneGeo g;
@@ -54,13 +63,12 @@ struct TileStream {
     stage = stage_lds;
     g = lane_geo<K>(l & 15, l >> 4);
     // chunk L = i*64 + lane -> tile row L / (2K) of the block, 16-byte piece L % (2K); it lands at stage byte 16 L,
-    // so each tile sits contiguously at stage byte 32K * row.  A lane past the last chunk still loads -- from beyond
-    // the buffer's end, which reads zeros -- so that every load is issued by every wave and the compiler's in-order
-    // load waits stay exact (a lane-conditional load becomes a branch it must assume skipped or taken).
+    // so each tile sits contiguously at stage byte 32K * row
 #pragma unroll
     for (int i = 0; i < LPB; i++) {
       const int L = i * 64 + l;
-      goff[i] = L < CHUNKS ? (L / (2 * K)) * row_bytes + (L % (2 * K)) * 16 : kOutOfRange;
+      glive[i] = L < CHUNKS;
+      goff[i] = glive[i] ? (L / (2 * K)) * row_bytes + (L % (2 * K)) * 16 : kOutOfRange;
     }
   }
 
@@ -68,7 +76,9 @@ struct TileStream {
     const int so = soff0 + min(b, nb - 1) * 8 * row_bytes;
 #pragma unroll
     for (int i = 0; i < LPB; i++)
-      buf[b][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, goff[i], so, 0));
+      buf[b][i] = ALL_LANES || glive[i]
+                      ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, goff[i], so, 0))
+                      : u32x4_t{0, 0, 0, 0};
   }
 
   // the first three blocks; call before staging the activations so their latency overlaps
@@ -86,7 +96,8 @@ struct TileStream {
     for (int b = 0; b < NB; b++) {
       uint8_t* st = stage + (b & 1) * STAGE;
 #pragma unroll
-      for (int i = 0; i < LPB; i++) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
+      for (int i = 0; i < LPB; i++)
+        if (ALL_LANES || glive[i]) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
       if (b + 3 < NB) issue(b + 3);
       const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
 #pragma unroll
@@ -110,7 +121,8 @@ struct TileStream {
     for (int b = 0; b < NB; b++) {
       uint8_t* st = stage + (b & 1) * STAGE;
 #pragma unroll
-      for (int i = 0; i < LPB; i++) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
+      for (int i = 0; i < LPB; i++)
+        if (ALL_LANES || glive[i]) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
       if (b + 3 < NB) issue(b + 3);
       const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
 #pragma unroll
