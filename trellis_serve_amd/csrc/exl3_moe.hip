@@ -209,12 +209,9 @@ __global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const vo
 // spilling; the others take what they need (P = 4 and K >= 5: 80-130 VGPRs; P = 4 is held to one workgroup per CU by
 // its LDS anyway).
 template <int K, int CB, int PHASE, int P, bool PRE, int NT>
-__global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) void moe_gemv_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
-                                                                uint16_t* __restrict__ gu,
-                                                                uint16_t* __restrict__ pre_dn_out,
-                                                                uint16_t* __restrict__ dn,
-                                                                float* partial,
-                                                                int* counters, int splits, int chunks) {
+__global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) void moe_gemv_kernel(
+    MoeArgs a, const void* __restrict__ x, int x_bf16, uint16_t* __restrict__ gu, uint16_t* __restrict__ pre_dn_out,
+    uint16_t* __restrict__ dn, float* partial, int* counters, int splits, int chunks) {
   typedef TileStream<K, CB, NT, PRE> Stream;  // the prepared-row chunk pipeline needs every lane loading
   constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -628,7 +625,8 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
                                 size_t workspace_bytes, void* stream) {
   EXL3_CHECK_ARG(x && y && topk_ids && topk_weights && w, "exl3_moe_forward: null pointer");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_moe_forward: K = %d / codebook = %d", K, codebook);
-  EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= kMoeMaxTopK, "exl3_moe_forward: tokens = %d, top_k = %d", tokens, top_k);
+  EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= kMoeMaxTopK, "exl3_moe_forward: tokens = %d, top_k = %d",
+                 tokens, top_k);
   EXL3_CHECK_ARG(num_experts >= 1 && num_experts <= 1024, "exl3_moe_forward: num_experts = %d (1..1024)", num_experts);
   EXL3_CHECK_ARG(hidden > 0 && hidden % 128 == 0 && inter > 0 && inter % 128 == 0,
                  "exl3_moe_forward: hidden = %d, inter = %d (multiples of 128)", hidden, inter);
