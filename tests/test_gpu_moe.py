@@ -258,3 +258,38 @@ def test_moe_slot_groups_and_passes_match_exact_layer(T):
         one = ops.moe_forward(xd[t:t + 1], idd[t:t + 1], wd[t:t + 1], st, 1).float()[0]
         assert ((y[t].float() - one).norm() / one.norm()).item() <= 1e-3, t
     assert torch.equal(ops.moe_forward(xd, idd, wd, st, 1), y)
+
+def _moe_cases(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        E = int(rng.integers(2, 17))
+        out.append((E, 128 * int(rng.integers(1, 5)), 128 * int(rng.integers(1, 5)), int(rng.choice([2, 3, 4, 5, 6, 8])),
+                    int(rng.integers(0, 3)), int(rng.integers(1, 49)), int(rng.integers(1, min(8, E) + 1))))
+    return out
+
+
+MOE_CASES = _moe_cases(2028, 12)
+
+
+@pytest.mark.parametrize("case", MOE_CASES, ids=[f"E{c[0]}-H{c[1]}-I{c[2]}-K{c[3]}-cb{c[4]}-T{c[5]}-top{c[6]}"
+                                                  for c in MOE_CASES])
+def test_moe_random_shapes_match_exact_layer(case):
+    """Seeded random MoE layers: experts 2-16, hidden and inter 128-512, every bit width and codebook, 1-48 tokens,
+    top-k 1-8 with about one id in ten unrouted (-1), against the float64 exact layer."""
+    from trellis_serve_amd import ops
+    E, H, I, K, cb, T, top_k = case
+    rng = np.random.default_rng(abs(hash(case)) % (1 << 32))
+    ex = _experts(rng, E, H, I, K)
+    x = (rng.standard_normal((T, H)) * 0.5).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:top_k] for _ in range(T)]).astype(np.int32)
+    ids[rng.random(ids.shape) < 0.1] = -1
+    w = rng.random((T, top_k)).astype(np.float32)
+    y = ops.moe_forward(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(),
+                        _stack(ex), cb).cpu().numpy()
+    ref = orc.moe_forward(x, ids, w, ex, K, cb)
+    if not np.abs(ref).max() > 0:  # every slot unrouted: a zero row
+        assert (y == 0).all()
+        return
+    nrel, mrel = _errs(y, ref)
+    assert nrel <= 2e-3 and mrel <= 2e-3, (case, nrel, mrel)
