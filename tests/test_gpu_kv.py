@@ -156,3 +156,32 @@ def test_kv_decode_shapes_on_one_workspace_and_repeatable():
         assert all((y[b] == 0).all() for b, L in enumerate(lens) if L == 0)
         for _ in range(3):
             assert torch.equal(_run(q, kc, vc, ks, vs, table, lens, bits, sm), first)
+
+
+def _kv_cases(seed, count):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(count):
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.integers(1, 17))
+        B = int(rng.integers(1, 9))
+        lens = tuple(int(v) for v in rng.integers(1, 3000, size=B))
+        out.append((lens, G * Hkv, Hkv, int(rng.choice([4, 8])), int(rng.integers(0, 3))))
+    return out
+
+
+KV_CASES = _kv_cases(2029, 12)
+
+
+@pytest.mark.parametrize("case", KV_CASES, ids=[f"B{len(c[0])}-L{max(c[0])}-q{c[1]}-kv{c[2]}-b{c[3]}" for c in KV_CASES])
+def test_kv_decode_random_shapes(case):
+    """Seeded random batches: 1-8 sequences of 1 … 2999 tokens, 1 / 2 / 4 / 8 KV heads with GQA groups of 1-16, 4 or
+    8 bits, 0-2 spare table columns, against the float64 closed form."""
+    lens, Hq, Hkv, bits, spare = case
+    max_pages = max(-(-L // PAGE) for L in lens) + spare
+    q, kc, vc, ks, vs, table = _case(abs(hash(case)) % (1 << 32), list(lens), Hq, Hkv, bits, max_pages=max_pages)
+    sm = D ** -0.5
+    y = _run(q, kc, vc, ks, vs, table, lens, bits, sm).cpu().numpy()
+    ref = orc.kv_decode_attention(q, kc, vc, ks, vs, table, np.asarray(lens, np.int32), bits, sm)
+    nrel, mrel = _errs(y, ref)
+    assert nrel <= 2e-3 and mrel <= 2e-3, (case, nrel, mrel)
