@@ -83,7 +83,7 @@ def _capture(torch, fn):
 def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int):
     """One graph holds R steps (step r: the 4 fused linears on rotating copy r).  Replays it ceil(steps / R) times
     after ceil(warmup / R) untimed replays; returns (steps timed, ms per step, per-layer us per launch).  Per-layer
-    times come from a graph of R launches of that layer alone, timed the same way."""
+    times come from a graph of R launches of that layer alone, timed the same way (same warmup)."""
     R = len(sets)
     names = list(LAYERS)
     outs = {nm: torch.empty((xs[nm].shape[0], sum(LAYERS[nm][1])), dtype=torch.float16, device=xs[nm].device)
@@ -114,7 +114,7 @@ def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int):
     for nm in names:
         g = _capture(torch, lambda nm=nm: run(range(R), [nm]))
         lreps = max(4, reps // 2)
-        per_layer[nm] = timed(g, lreps, 2) / (lreps * R)
+        per_layer[nm] = timed(g, lreps, -(-warmup // R)) / (lreps * R)
     return reps * R, total / (reps * R), per_layer
 
 
