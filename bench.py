@@ -237,6 +237,7 @@ def bench_prefill(torch, ops, dev) -> dict:
     g = torch.Generator(device="cpu").manual_seed(11)
     cases = [(3, 1, 512), (3, 1, 2048), (3, 1, 8192), (2, 0, 2048), (4, 2, 2048), (5, 1, 2048), (6, 0, 2048),
              (8, 2, 2048)]
+    ops.reserve_prefill(dev, max(M for _, _, M in cases), k, n, 1)
     names = {0: "3inst", 1: "mcg", 2: "mul1"}
     out = {}
     for K, cb, M in cases:
@@ -340,6 +341,7 @@ def bench_moe(torch, ops, dev) -> dict:
         return d
 
     sets = [experts() for _ in range(copies)]
+    ops.reserve_moe(dev, 256, top_k, E, H, I, K, K)
     out = {}
     for T in (1, 16, 256):
         routes = []
@@ -367,6 +369,7 @@ def bench_kv(torch, ops, dev) -> dict:
     cache copies keep >= 512 MB in play at 4k.  Bytes = codes + scales + page table + q/out."""
     B, Hq, Hkv, D = 16, 40, 8, 128
     g = torch.Generator(device="cpu").manual_seed(13)
+    ops.reserve_kv(dev, B, Hq, Hkv, 32768 // 16)
     out = {}
     for L in (4096, 32768):
         for bits in (8, 4):
@@ -500,8 +503,13 @@ def main() -> int:
     def xs_for(M):
         return {nm: torch.randn((M, k), generator=g).half().to(dev) for nm, (k, _) in LAYERS.items()}
 
+    row_list = [args.rows] + [int(v) for v in args.extra_rows.split(",") if v and int(v) != args.rows]
+    # load-time reservation, as an engine does before capturing graphs: one workspace per kind and device, sized for
+    # the largest call, so no captured graph ever holds a buffer that a larger call would replace
+    for k, ns in LAYERS.values():
+        ops.reserve_linear(dev, max(row_list), k, sum(ns), K_BITS)
     results = {}
-    for M in [args.rows] + [int(v) for v in args.extra_rows.split(",") if v and int(v) != args.rows]:
+    for M in row_list:
         xs = xs_for(M)
         steps = args.steps if M == args.rows else max(20, args.steps // 4)
         steps, ms_step, per_layer = time_layer_set(torch, ops, sets, xs, steps, args.warmup)

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 1
+#define EXL3_ABI_VERSION 2
 
 enum {
   EXL3_OK = 0,
@@ -109,7 +109,9 @@ int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_s
 
 /* ---- MoE grouped experts (subsystem 5a) --------------------------------------------------------------------------- */
 /* Stacked expert weights of one MoE layer (SiLU-gated, no routed scaling: the contract of the reference's
- * Exl3MoEMethod, cuda/src/sglang_exl3/sglang_glue/moe.py:109-119).  All experts share K and the codebook. */
+ * Exl3MoEMethod, cuda/src/sglang_exl3/sglang_glue/moe.py:109-119).  All experts share the codebook; gate and up share
+ * one bitrate K_gate_up, down has its own K_down (the reference checks only gate K == up K, moe.py:148-152, and runs
+ * the two bitrates separately, cuda/src/sglang_exl3/kernels/reference.py:123-149). */
 typedef struct exl3_moe_weights {
   const void* gate_trellis; /* int16 [E][H/16][I/16][16K] */
   const void* up_trellis;   /* int16 [E][H/16][I/16][16K] */
@@ -126,7 +128,8 @@ typedef struct exl3_moe_weights {
  * partials).  The
  * counter region (EXL3_WORKSPACE_COUNTER_BYTES, holding num_experts * (2 inter + hidden) / 128 counters) must be
  * zero before the first use; every call leaves it zero. */
-size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K);
+size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K_gate_up,
+                                int K_down);
 /* y[t] = sum_j w[t, j] * down_e(fp16(silu(gate_e(x[t])) * up_e(x[t]))), e = topk_ids[t, j]; every linear is an EXL3
  * linear with its own suh / svh; fp32 combine in slot order; ids outside [0, E) are skipped.  x fp16|bf16 [T, H],
  * topk_ids int32 [T, top_k] (top_k <= 64), topk_weights fp32 [T, top_k], y fp16|bf16 [T, H].  Replaces the five
@@ -134,8 +137,9 @@ size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidd
  * moe_combine; cuda/csrc/exl3_marlin_moe.cu:376-499) and the align step (exl3_marlin_moe.cu:532-594) with four
  * launches (three for a single token).  Calls that share a workspace must not overlap. */
 int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids, const void* topk_weights,
-                     int top_k, int num_experts, int inter, const exl3_moe_weights* weights_host, int K, int codebook,
-                     void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
+                     int top_k, int num_experts, int inter, const exl3_moe_weights* weights_host, int K_gate_up,
+                     int K_down, int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* ---- Quantized-KV paged decode attention (subsystem 5b) ------------------------------------------------------------ */
 /* The reference has no quantized-KV decode kernel: its nearest relative is the paged fp8 gather + dequant + blockwise

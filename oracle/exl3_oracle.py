@@ -202,17 +202,24 @@ def moe_forward(x, topk_ids, topk_w, experts, K, cb, dtype=np.float64, w_cache=N
         y_t = sum_j w[t, j] * d_slot   (slot order, as exl3_marlin_moe.cu:262-292)
     `experts[e]` = dict(gate=(trellis, suh, svh), up=(...), down=(...)).  Evaluated in `dtype` (float64 = the
     exact layer of tools/moe_parity_sm86.py:76-89).  Slots whose id is outside [0, E) are skipped
-    (exl3_marlin_moe.cu:274)."""
+    (exl3_marlin_moe.cu:274).  Each projection runs at its own bitrate, read from its trellis (16K int16 per tile;
+    the reference's gate/up and down bitrates, cuda/src/sglang_exl3/kernels/reference.py:123-149); `K`, when not
+    None, must agree with every projection."""
     tokens, hidden = x.shape
     top_k = topk_ids.shape[1]
     y = np.zeros((tokens, hidden), dtype=dtype)
     w_cache = {} if w_cache is None else w_cache
 
+    def bits(e, proj):
+        kp = experts[e][proj][0].shape[-1] // 16
+        assert K is None or K == kp, f"expert {e} {proj}: trellis holds K = {kp}, caller said {K}"
+        return kp
+
     def w_of(e, proj):
         key = (e, proj)
         if key not in w_cache:
             t, _, _ = experts[e][proj]
-            w_cache[key] = reconstruct_inner(t, K, cb)
+            w_cache[key] = reconstruct_inner(t, bits(e, proj), cb)
         return w_cache[key]
 
     for t in range(tokens):
@@ -221,10 +228,10 @@ def moe_forward(x, topk_ids, topk_w, experts, K, cb, dtype=np.float64, w_cache=N
             if e < 0 or e >= len(experts):
                 continue
             xt = x[t:t + 1].astype(dtype)
-            g = linear_forward(xt, *experts[e]["gate"], K, cb, w_inner=w_of(e, "gate"), dtype=dtype)
-            u = linear_forward(xt, *experts[e]["up"], K, cb, w_inner=w_of(e, "up"), dtype=dtype)
+            g = linear_forward(xt, *experts[e]["gate"], bits(e, "gate"), cb, w_inner=w_of(e, "gate"), dtype=dtype)
+            u = linear_forward(xt, *experts[e]["up"], bits(e, "up"), cb, w_inner=w_of(e, "up"), dtype=dtype)
             a = (g / (1.0 + np.exp(-g))) * u
-            d = linear_forward(a, *experts[e]["down"], K, cb, w_inner=w_of(e, "down"), dtype=dtype)
+            d = linear_forward(a, *experts[e]["down"], bits(e, "down"), cb, w_inner=w_of(e, "down"), dtype=dtype)
             y[t] += dtype(topk_w[t, j]) * d[0]
     return y
 

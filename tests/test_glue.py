@@ -157,7 +157,8 @@ def test_moe_loading(ckpt):
     assert tuple(ex["up_suh"].shape) == (E, H) and tuple(ex["down_svh"].shape) == (E, H)
     np.testing.assert_array_equal(ex["up_trellis"][2].cpu().numpy(),
                                   tensors["model.language_model.layers.1.mlp.experts.2.up_proj.trellis"])
-    assert layer.exl3_codebook == 1 and layer.exl3_bits == 3 and not hasattr(layer, "w13_trellis")
+    assert layer.exl3_codebook == 1 and layer.exl3_bits == {"gate": 3, "up": 3, "down": 3}
+    assert not hasattr(layer, "w13_trellis")
     with pytest.raises(NotImplementedError, match="SiLU"):
         method.create_moe_runner(layer, types.SimpleNamespace(activation="gelu"))
     with pytest.raises(NotImplementedError, match="routed_scaling_factor"):

@@ -222,7 +222,7 @@ def test_workspace_shared_by_calls_of_different_shapes(coracle):
     """One workspace serves calls of any shapes: a call with many k-splits leaves fp32 partials behind its counters;
     a later call with more output column blocks must still see zero counters (they sit in a fixed region)."""
     ops = _ops()
-    ops._workspace.clear()
+    ops.release_workspaces()
     rng = np.random.default_rng(10)
     K, cb = 3, 1
     for k, n, M in ((8192, 128, 16), (256, 12800, 1), (1024, 4096, 3), (8192, 128, 16)):

@@ -143,7 +143,7 @@ def test_kv_decode_shapes_on_one_workspace_and_repeatable():
     """Calls of different batch / head / length shapes on one workspace, each against the closed form, a
     zero-length sequence in the batch (its rows are zero), and repeated calls bit-identical."""
     from trellis_serve_amd import ops
-    ops._kv_ws.clear()
+    ops.release_workspaces()
     sm = D ** -0.5
     for seed, lens, Hq, Hkv, bits in ((81, [4096, 0, 700], 40, 8, 8), (82, [33], 8, 2, 4), (83, [1500, 2049], 16, 4, 8)):
         q, kc, vc, ks, vs, table = _case(seed, lens, Hq, Hkv, bits)

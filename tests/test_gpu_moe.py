@@ -11,12 +11,12 @@ from oracle import exl3_oracle as orc
 pytestmark = pytest.mark.gpu
 
 
-def _experts(rng, E, H, I, K):
-    def mat(k, n):
-        return (rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int16),
+def _experts(rng, E, H, I, K, K_down=None):
+    def mat(k, n, bits):
+        return (rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * bits), dtype=np.int16),
                 np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16),
                 np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16))
-    return [dict(gate=mat(H, I), up=mat(H, I), down=mat(I, H)) for _ in range(E)]
+    return [dict(gate=mat(H, I, K), up=mat(H, I, K), down=mat(I, H, K_down or K)) for _ in range(E)]
 
 
 def _stack(ex):
@@ -79,7 +79,7 @@ def test_moe_workspace_shared_by_calls_of_different_shapes():
     """A call with many slots, then calls with fewer slots and another layer shape, on one workspace: the split
     counters sit in a fixed region, so no call reads an earlier call's rows or partials as counters."""
     from trellis_serve_amd import ops
-    ops._moe_ws.clear()
+    ops.release_workspaces()
     rng = np.random.default_rng(11)
     for E, H, I, T, top_k in ((16, 256, 256, 64, 4), (16, 256, 256, 1, 4), (8, 512, 128, 3, 2), (16, 256, 256, 9, 4)):
         ex = _experts(rng, E, H, I, 3)
@@ -293,3 +293,54 @@ def test_moe_random_shapes_match_exact_layer(case):
         return
     nrel, mrel = _errs(y, ref)
     assert nrel <= 2e-3 and mrel <= 2e-3, (case, nrel, mrel)
+
+
+@pytest.mark.parametrize("K, K_down", [(3, 4), (4, 3), (2, 6)])
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_moe_down_bitrate_differs_from_gate_up(K, K_down, T):
+    """A checkpoint may store down_proj at another bitrate than gate_proj / up_proj (the reference requires only gate
+    K == up K, cuda/src/sglang_exl3/sglang_glue/moe.py:148-152, and runs bits_gate_up and bits_down separately,
+    kernels/reference.py:123-149).  Single token (slot mode), a few tokens (P = 1) and 40 tokens (P = 2, the GLU
+    folded into the gate/up reducer) against the float64 exact layer, every codebook."""
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(7000 + 10 * K + K_down + T)
+    E, H, I, top_k = 8, 256, 384, 4
+    ex = _experts(rng, E, H, I, K, K_down)
+    st = _stack(ex)
+    assert st["down_trellis"].shape[-1] == 16 * K_down and st["gate_trellis"].shape[-1] == 16 * K
+    x = (rng.standard_normal((T, H)) * 0.5).astype(np.float16)
+    ids = np.stack([rng.permutation(E)[:top_k] for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, top_k)).astype(np.float32)
+    for cb in (0, 1, 2):
+        y = ops.moe_forward(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), st,
+                            cb).cpu().numpy()
+        nrel, mrel = _errs(y, orc.moe_forward(x, ids, w, ex, None, cb))
+        assert nrel <= 2e-3 and mrel <= 2e-3, (K, K_down, T, cb, nrel, mrel)
+
+
+def test_moe_full_shape_single_token_mixed_bitrates(coracle):
+    """BASELINE configs[3] shape (128 experts, top-8, hidden 2048, inter 768, MCG) with gate/up at K = 3 and down at
+    K = 4: one token against the exact layer (C reconstruct of every touched expert)."""
+    from conftest import c_reconstruct
+    from trellis_serve_amd import ops
+    rng = np.random.default_rng(49)
+    E, H, I, top_k, cb = 128, 2048, 768, 8, 1
+    bits = {"gate": 3, "up": 3, "down": 4}
+    st = {}
+    for proj, (kk, nn) in (("gate", (H, I)), ("up", (H, I)), ("down", (I, H))):
+        st[f"{proj}_trellis"] = torch.from_numpy(
+            rng.integers(-32768, 32768, size=(E, kk // 16, nn // 16, 16 * bits[proj]), dtype=np.int16)).cuda()
+        st[f"{proj}_suh"] = torch.from_numpy(np.where(rng.random((E, kk)) < 0.5, -1.0, 1.0).astype(np.float16)).cuda()
+        st[f"{proj}_svh"] = torch.from_numpy(np.where(rng.random((E, nn)) < 0.5, -1.0, 1.0).astype(np.float16)).cuda()
+    x = (rng.standard_normal((1, H)) * 0.05).astype(np.float16)
+    ids = rng.permutation(E)[:top_k].astype(np.int32)[None]
+    w = rng.random((1, top_k)).astype(np.float32)
+    ex, cache = [None] * E, {}
+    for e in ids[0].tolist():
+        ex[e] = {p: tuple(st[f"{p}_{part}"][e].cpu().numpy() for part in ("trellis", "suh", "svh"))
+                 for p in ("gate", "up", "down")}
+        for p in ("gate", "up", "down"):
+            cache[(e, p)] = c_reconstruct(coracle, ex[e][p][0], bits[p], cb)
+    y = ops.moe_forward(torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), st, cb)
+    nrel, mrel = _errs(y.cpu().numpy(), orc.moe_forward(x, ids, w, ex, None, cb, w_cache=cache))
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)

@@ -183,24 +183,34 @@ def test_weight_orig_matches_reference_and_forward(golden):
 
 # ---- MoE and KV-attention restatements -------------------------------------------------------------------------
 
-def _tiny_experts(rng, E, H, I, K, cb):
-    def mat(k, n):
-        return (rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int16),
+def _tiny_experts(rng, E, H, I, K, cb, K_down=None):
+    def mat(k, n, bits):
+        return (rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * bits), dtype=np.int16),
                 np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float16),
                 np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float16))
-    return [dict(gate=mat(H, I), up=mat(H, I), down=mat(I, H)) for _ in range(E)]
+    return [dict(gate=mat(H, I, K), up=mat(H, I, K), down=mat(I, H, K_down or K)) for _ in range(E)]
 
 
-def test_moe_forward_equals_original_basis_evaluation():
+@pytest.mark.parametrize("K, K_down", [(3, 3), (3, 4), (2, 6)])
+def test_moe_forward_equals_original_basis_evaluation(K, K_down):
+    """The routed layer against a direct evaluation with the original-basis weights, gate/up and down at their own
+    bitrates (the reference runs bits_gate_up and bits_down separately, kernels/reference.py:123-149)."""
     rng = np.random.default_rng(3)
-    E, H, I, K, cb, T, top_k = 4, 128, 128, 3, orc.CB_MCG, 3, 2
-    ex = _tiny_experts(rng, E, H, I, K, cb)
+    E, H, I, cb, T, top_k = 4, 128, 128, orc.CB_MCG, 3, 2
+    ex = _tiny_experts(rng, E, H, I, K, cb, K_down)
     x = rng.standard_normal((T, H)).astype(np.float16)
     ids = np.array([[0, 2], [3, 0], [1, 2]], dtype=np.int32)
     w = rng.random((T, top_k)).astype(np.float32)
-    y = orc.moe_forward(x, ids, w, ex, K, cb)
+    y = orc.moe_forward(x, ids, w, ex, None, cb)
+    if K == K_down:
+        assert np.array_equal(y, orc.moe_forward(x, ids, w, ex, K, cb))
+    else:
+        with pytest.raises(AssertionError):
+            orc.moe_forward(x, ids, w, ex, K, cb)
+    bits = {"gate": K, "up": K, "down": K_down}
+    W = {(e, p): orc.weight_orig(*ex[e][p], bits[p], cb).astype(np.float64) for e in range(E)
+         for p in ("gate", "up", "down")}
     want = np.zeros((T, H))
-    W = {(e, p): orc.weight_orig(*ex[e][p], K, cb).astype(np.float64) for e in range(E) for p in ("gate", "up", "down")}
     for t in range(T):
         for j in range(top_k):
             e = ids[t, j]

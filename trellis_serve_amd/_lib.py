@@ -53,9 +53,9 @@ _SIGNATURES: dict[str, tuple] = {
     "exl3_gemm_rotated": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _P, _SZ, _P]),
     "exl3_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "exl3_linear_prefill": (_I, [_P, _I, _I, _I, ctypes.POINTER(Exl3Shard), _I, _I, _I, _P, _I, _P, _SZ, _P]),
-    "exl3_moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I]),
-    "exl3_moe_forward": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, ctypes.POINTER(Exl3MoeWeights), _I, _I, _P, _I,
-                              _P, _SZ, _P]),
+    "exl3_moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I]),
+    "exl3_moe_forward": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, ctypes.POINTER(Exl3MoeWeights), _I, _I, _I, _P,
+                              _I, _P, _SZ, _P]),
     "exl3_kv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "exl3_kv_decode_attention": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, ctypes.c_float, _P,
                                       _P, _SZ, _P]),

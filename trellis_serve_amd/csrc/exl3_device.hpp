@@ -23,6 +23,7 @@ enum Codebook : int { CB_3INST = 0, CB_MCG = 1, CB_MUL1 = 2 };
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t uint2_t __attribute__((ext_vector_type(2)));
 
@@ -149,6 +150,25 @@ __device__ __forceinline__ half4_t decode_group(uint32_t w0, uint32_t w1, const 
   p.x = cb_pair<CB>(s[0], s[1]);
   p.y = cb_pair<CB>(s[2], s[3]);
   return __builtin_bit_cast(half4_t, p);
+}
+
+// The lane's four weights as their unsummed fp16 halves, for the GEMV: dword e of the result is the masked hash of
+// state e, i.e. the pair [lo_e, hi_e] whose fp16 sum is weight e (MCG / 3INST only).  As the 8-half B operand of
+// v_mfma_f32_16x16x32_f16 against activations staged twice ([a0, a0, a1, a1, ...]) the matrix core forms
+// a*lo + a*hi in fp32, where the exact layer has a * fp16(lo + hi): the mask keeps both halves' exponent fields in
+// 12..15 (magnitudes in [1/8, 2)), so lo + hi is exact in fp32 and differs from the rounded weight by at most half
+// an fp16 ulp of it, inside the layer tolerance.  A one-hot activation row reads fp16(lo + hi) back exactly: the
+// sum of two exact products, rounded once to fp16, is the rounded weight (__hadd rounds the same exact sum).  This
+// drops the per-weight fp16 add, a quarter of the decode's VALU work.
+template <int K, int CB>
+__device__ __forceinline__ half8_t decode_group_halves(uint32_t w0, uint32_t w1, const LaneGeo& g) {
+  static_assert(CB != CB_MUL1, "MUL1 has no two-halves form: its weight is one rounded FMA");
+  uint32_t s[4];
+  group_states<K>(w0, w1, g, s);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = {cb_hash_masked<CB>(s[0]), cb_hash_masked<CB>(s[1]), cb_hash_masked<CB>(s[2]),
+                   cb_hash_masked<CB>(s[3])};
+  return __builtin_bit_cast(half8_t, v);
 }
 
 // ---- fp16 / bf16 boundary conversions (torch value conversions, RNE) -----------------------------------------

@@ -188,12 +188,15 @@ constexpr int kGemvThreads = kGemvWaves * 64;
 constexpr int kCoherentDevice = 1 << 4;  // buffer cache policy sc1: device-scope coherent access
 constexpr int kWaitVmcnt0 = 0x0F70;      // s_waitcnt vmcnt(0) (expcnt, lgkmcnt unconstrained)
 
-// LDS bytes of the GEMV: staged activations (M rows of NT*16 + 4 halves), then per wave two block stages of 256*K
-// bytes; at least 16 * 128 fp32 for the epilogue reduce
-__host__ __device__ constexpr int gemv_a_bytes(int M, int NT) { return ((M * (NT * 16 + 4) * 2) + 15) & ~15; }
-__host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K) {
-  return gemv_a_bytes(M, NT) + kGemvWaves * stream_lds_bytes(K) > kGemvThreads * 16
-             ? gemv_a_bytes(M, NT) + kGemvWaves * stream_lds_bytes(K)
+// LDS bytes of the GEMV: staged activations (M rows of NT*16 + 4 halves, or twice that with every value staged
+// twice: NT*32 + 8), then per wave two block stages of 256*K bytes; at least 16 * 128 fp32 for the epilogue reduce
+__host__ __device__ constexpr int gemv_mstride(int NT, bool dup) { return dup ? NT * 32 + 8 : NT * 16 + 4; }
+__host__ __device__ constexpr int gemv_a_bytes(int M, int NT, bool dup) {
+  return ((M * gemv_mstride(NT, dup) * 2) + 15) & ~15;
+}
+__host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K, bool dup) {
+  return gemv_a_bytes(M, NT, dup) + kGemvWaves * stream_lds_bytes(K) > kGemvThreads * 16
+             ? gemv_a_bytes(M, NT, dup) + kGemvWaves * stream_lds_bytes(K)
              : kGemvThreads * 16;
 }
 
@@ -204,8 +207,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
                                                              int M, int k, int splits, float* partial,
                                                              int* counters, void* __restrict__ y,
                                                              int y_bf16, int n_total, int pre_rows = 0) {
-  typedef TileStream<K, CB, NT> Stream;
+  typedef TileStream<K, CB, NT, false, true> Stream;
   constexpr int NB = Stream::NB;
+  constexpr bool DUP = Stream::DUP;  // activations staged twice for the two-halves decode (MCG, 3INST)
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
@@ -213,7 +217,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   const int s = find_shard(sa, blk);
   const int kb0 = split * NB;
   const int nb = min(k >> 7, kb0 + NB) - kb0;  // blocks of this split holding data (1..NB)
-  const int mstride = NT * 16 + 4;
+  constexpr int mstride = gemv_mstride(NT, DUP);
+  // one activation value into the staging area (twice with DUP: a_slot_dup is 2 a_slot inside a row)
+  auto stage1 = [&](int p, int m, _Float16 h) {
+    if constexpr (DUP)
+      *reinterpret_cast<half2_t*>(xs + a_slot_dup(p, m, mstride)) = half2_t{h, h};
+    else
+      xs[a_slot(p, m, mstride)] = h;
+  };
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
@@ -237,7 +248,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
   Stream stream;
   stream.init(sa.trellis[s], (k >> 4) * tn * 32 * K, tn, (blk - sa.blk0[s]) * kGemvWaves + w, kb0, nb,
-              lds + gemv_a_bytes(M, NT) + w * Stream::LDS_BYTES, l);
+              lds + gemv_a_bytes(M, NT, DUP) + w * Stream::LDS_BYTES, l);
   stream.start();
 
   if constexpr (PRE) {
@@ -256,7 +267,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
     for (int it = 0; it < IT; it++) {
       const int u = hw + it * 2 * kGemvWaves;
       const int m = u / NB, b = u - m * NB;
-      if (u < M * NB) *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
+      if (u < M * NB) {
+        if constexpr (DUP) {  // the 4 staged halves, each twice
+          uint32_t d[4] = {__builtin_amdgcn_perm(v[it].x, v[it].x, 0x01000100u),
+                           __builtin_amdgcn_perm(v[it].x, v[it].x, 0x03020302u),
+                           __builtin_amdgcn_perm(v[it].y, v[it].y, 0x01000100u),
+                           __builtin_amdgcn_perm(v[it].y, v[it].y, 0x03020302u)};
+          *reinterpret_cast<u32x4_t*>(xs + m * mstride + b * 256 + 8 * t) = u32x4_t{d[0], d[1], d[2], d[3]};
+        } else {
+          *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
+        }
+      }
     }
   } else if (single) {
     if (hw < M * NB) {
@@ -274,7 +295,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
+      for (int i = 0; i < 4; i++) stage1(b * 128 + 4 * t + i, m, h[i]);
     }
   } else {
     for (int u = hw; u < M * NB; u += 2 * kGemvWaves) {
@@ -293,13 +314,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
+      for (int i = 0; i < 4; i++) stage1(b * 128 + 4 * t + i, m, h[i]);
     }
   }
   __syncthreads();
 
   // A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored
-  const float4_t acc = stream.run(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j);
+  float4_t acc;
+  if constexpr (DUP)
+    acc = stream.run_dup(reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j);
+  else
+    acc = stream.run(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j);
 
 
   // this split's partial; C layout: lane l holds rows 4(l/16) + r, column l % 16.  Partials cross XCDs (each XCD
@@ -387,19 +412,21 @@ static int gemv_target_wgs(int M) {
   return env ? env : M >= 8 ? 768 : 1536;
 }
 
-// pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there
-static GemvPlan gemv_plan(int k, int n_total, int M, int K, bool pre = false) {
+// pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there.
+// cb: MCG / 3INST stage the activations twice (more LDS per tile row)
+static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = false) {
   const int kb = k / 128, nblk = n_total / 128;
+  const bool dup = cb != CB_MUL1;
   int nt = 16;
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
     if (pre && cand > 32) continue;
-    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs(M) && gemv_lds_bytes(M, cand, K) <= kGemvMaxLds) {
+    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs(M) && gemv_lds_bytes(M, cand, K, dup) <= kGemvMaxLds) {
       nt = cand;
       break;
     }
   }
-  return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(M, nt, K)};
+  return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(M, nt, K, dup)};
 }
 
 // workspace layout: [counter region: one int per 128-column block, zero between calls][fp32 partials]; the region
@@ -463,13 +490,16 @@ static bool gemv_pre(int rows, int k, int n_total) {
   return rows >= kGemvPreRows && (size_t)(n_total / 128) * rows * (k / 128) >= kGemvPreUnits;
 }
 
-// workspace layout: [counter region][fp32 partials of the largest 16-row launch][rotated rows, when gemv_pre]
+// workspace layout: [counter region][fp32 partials of the largest 16-row launch][rotated rows, when gemv_pre]; the
+// size does not depend on the codebook (the largest plan of either staging form)
 static size_t gemv_partial_bytes(int rows, int k, int n_total, int K) {
   size_t need = 0;
   for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
     if (M == 0) continue;
-    const GemvPlan pl = gemv_plan(k, n_total, M, K, gemv_pre(rows, k, n_total));
-    need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
+    for (int cb : {(int)CB_MCG, (int)CB_MUL1}) {
+      const GemvPlan pl = gemv_plan(k, n_total, M, K, cb, gemv_pre(rows, k, n_total));
+      need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
+    }
   }
   return (need + 255) & ~(size_t)255;
 }
@@ -494,7 +524,7 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
   }
   for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
     const int M = std::min(kGemvRows, rows - r0);
-    const GemvPlan pl = gemv_plan(k, n_total, M, K, pre);
+    const GemvPlan pl = gemv_plan(k, n_total, M, K, cb, pre);
     const dim3 grid(n_total / 128, pl.splits);
     const void* xr = static_cast<const uint8_t*>(pre ? (const void*)xh : x) + (size_t)r0 * k * 2;
     void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
@@ -619,3 +649,4 @@ extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* tr
   sa.count = 1;
   return launch_gemv(sa, xh, false, false, rows, k, K, codebook, n, workspace, out, false, as_stream(stream));
 }
+

@@ -545,14 +545,14 @@ struct MoePlan {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I, int K) {
+static MoePlan moe_plan(int tokens, int top_k, int E, int H, int I, int K_gu, int K_dn) {
   MoePlan p{};
   const int slots = tokens * top_k;
   p.slot_mode = tokens == 1 && slots <= E;
   const int rows = p.slot_mode ? slots : std::max(1, std::min(E, slots));
   p.nt = 16;  // 32 measured slower with 256 tokens, equal with 16
-  p.gu = moe_phase_plan(slots, rows, 2 * I / 128, H, K, p.nt);
-  p.dn = moe_phase_plan(slots, rows, H / 128, I, K, p.nt);
+  p.gu = moe_phase_plan(slots, rows, 2 * I / 128, H, K_gu, p.nt);
+  p.dn = moe_phase_plan(slots, rows, H / 128, I, K_dn, p.nt);
   // enough groups that an expert with a typical-to-high slot count (mean + ~2.5 sd of a binomial count) is one pass
   const double mean = (double)slots / rows;
   const double high = mean + 2.5 * std::sqrt(mean);
@@ -613,18 +613,20 @@ static void launch_moe_gemv(const MoePlan& p, const MoePhase& ph, dim3 grid, con
 
 using namespace exl3;
 
-extern "C" size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int K) {
+extern "C" size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter,
+                                           int K_gate_up, int K_down) {
   if (tokens <= 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || inter <= 0) return 0;
   if ((int64_t)num_experts * (2 * inter + hidden) / 128 > kMaxCounters) return 0;
-  return moe_plan(tokens, top_k, num_experts, hidden, inter, K).total;
+  return moe_plan(tokens, top_k, num_experts, hidden, inter, K_gate_up, K_down).total;
 }
 
 extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids,
                                 const void* topk_weights, int top_k, int num_experts, int inter,
-                                const exl3_moe_weights* w, int K, int codebook, void* y, int y_bf16, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+                                const exl3_moe_weights* w, int K_gate_up, int K_down, int codebook, void* y,
+                                int y_bf16, void* workspace, size_t workspace_bytes, void* stream) {
   EXL3_CHECK_ARG(x && y && topk_ids && topk_weights && w, "exl3_moe_forward: null pointer");
-  EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_moe_forward: K = %d / codebook = %d", K, codebook);
+  EXL3_CHECK_ARG(valid_bits(K_gate_up) && valid_bits(K_down) && valid_cb(codebook),
+                 "exl3_moe_forward: K gate/up = %d, K down = %d, codebook = %d", K_gate_up, K_down, codebook);
   EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= kMoeMaxTopK, "exl3_moe_forward: tokens = %d, top_k = %d",
                  tokens, top_k);
   EXL3_CHECK_ARG(num_experts >= 1 && num_experts <= 1024, "exl3_moe_forward: num_experts = %d (1..1024)", num_experts);
@@ -633,14 +635,15 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   EXL3_CHECK_ARG(w->gate_trellis && w->up_trellis && w->down_trellis && w->gate_suh && w->gate_svh && w->up_suh &&
                      w->up_svh && w->down_suh && w->down_svh,
                  "exl3_moe_forward: null expert tensor");
-  EXL3_CHECK_ARG((int64_t)hidden * inter * K / 8 <= INT32_MAX, "exl3_moe_forward: expert matrix too large");
+  EXL3_CHECK_ARG((int64_t)hidden * inter * std::max(K_gate_up, K_down) / 8 <= INT32_MAX,
+                 "exl3_moe_forward: expert matrix too large");
   EXL3_CHECK_ARG((int64_t)num_experts * (2 * inter + hidden) / 128 <= kMaxCounters,
                  "exl3_moe_forward: %d experts x (2 x %d + %d) / 128 split counters exceed %d", num_experts, inter,
                  hidden, kMaxCounters);
   if (tokens == 0) return EXL3_OK;
   const int slots = tokens * top_k;
   EXL3_CHECK_ARG((int64_t)slots * std::max(2 * inter, hidden) <= INT32_MAX / 4, "exl3_moe_forward: too many slots");
-  const MoePlan p = moe_plan(tokens, top_k, num_experts, hidden, inter, K);
+  const MoePlan p = moe_plan(tokens, top_k, num_experts, hidden, inter, K_gate_up, K_down);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= p.total, "exl3_moe_forward: workspace %zu bytes, need %zu",
                  workspace_bytes, p.total);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -687,9 +690,14 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
     EXL3_CHECK_LAUNCH();
   }
   const int rows = a.slot_mode ? slots : std::min(num_experts, slots);
-  bool ok = EXL3_MOE_DISPATCH(K, codebook, {
+  // gate/up and down run at their own bitrates (a checkpoint may store down at another K than gate and up)
+  bool ok = EXL3_MOE_DISPATCH(K_gate_up, codebook, {
     launch_moe_gemv<kK, kCB, 0>(p, p.gu, dim3(2 * inter / 128, rows), a, x, x_bf16, gu, pre_dn, dn, partial,
                                 cnt_gu, st);
+  });
+  if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_moe_forward: unsupported K/codebook");
+  EXL3_CHECK_LAUNCH();
+  ok = EXL3_MOE_DISPATCH(K_down, codebook, {
     launch_moe_gemv<kK, kCB, 1>(p, p.dn, dim3(hidden / 128, rows), a, x, x_bf16, gu, pre_dn, dn, partial, cnt_dn,
                                 st);
   });

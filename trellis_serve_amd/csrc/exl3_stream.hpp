@@ -30,8 +30,15 @@ __host__ __device__ constexpr int stream_lds_bytes(int K, bool all_lanes = false
 // must assume taken or skipped, which turns its in-order load waits into vmcnt(0) in a loop that keeps loads in
 // flight across iterations (the MoE chunk pipeline); straight-line callers (the dense GEMV) keep the lane mask, which
 // spends fewer address cycles (48 of 64 lanes at K = 3).
-template <int K, int CB, int NT, bool ALL_LANES = false>
+// HALVES (the dense GEMV): MCG and 3INST tiles go to the matrix core as their unsummed fp16 halves
+// (decode_group_halves, v_mfma_f32_16x16x32_f16) against activations staged twice (a_slot_dup); MUL1 tiles, and every
+// tile without HALVES, as rounded fp16 weights (v_mfma_f32_16x16x16_f16, a_slot).
+template <int CB, bool HALVES>
+__host__ __device__ constexpr bool stream_dup() { return HALVES && CB != CB_MUL1; }
+
+template <int K, int CB, int NT, bool ALL_LANES = false, bool HALVES = false>
 struct TileStream {
+  static constexpr bool DUP = stream_dup<CB, HALVES>();
   static constexpr int NB = NT / 8;               // 128-row blocks
   static constexpr int CHUNKS = 16 * K;           // 16-byte chunks in the 8 tiles of one block column
   static constexpr int LPB = (CHUNKS + 63) / 64;  // wave-wide gathers per block
@@ -112,6 +119,30 @@ struct TileStream {
     return acc0 + acc1;
   }
 
+  // DUP form of run: ap is the lane's 8-half A fragment ([a, a] per row, a_slot_dup) for tile row 0, 4 half8 per
+  // tile row.
+  __device__ __forceinline__ float4_t run_dup(const half8_t* ap) {
+    float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      uint8_t* st = stage + (b & 1) * STAGE;
+#pragma unroll
+      for (int i = 0; i < LPB; i++)
+        if (ALL_LANES || glive[i]) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
+      if (b + 3 < NB) issue(b + 3);
+      const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const half8_t bv = decode_group_halves<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
+        if (u & 1)
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[(b * 8 + u) * 4], bv, acc1, 0, 0, 0);
+        else
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[(b * 8 + u) * 4], bv, acc0, 0, 0, 0);
+      }
+    }
+    return acc0 + acc1;
+  }
+
   // For up to P groups of 16 A rows sharing each decoded tile (groups <= P active, uniform): group p reads its
   // fragment gstride half4 after group p-1's and accumulates into acc[p] (one chain per group: the decode between two
   // MFMAs of a group covers their dependency).
@@ -144,6 +175,14 @@ struct TileStream {
 __device__ __forceinline__ int a_slot(int p, int m, int mstride) {
   const int r = p & 15;
   return m * mstride + ((p >> 4) << 4) + (((r & 7) >> 1) << 2) + ((r & 1) | ((r >> 3) << 1));
+}
+
+// The same order with every value stored twice (a_slot_dup and a_slot_dup + 1): lane (m, q) reads its 8-half
+// fragment [a0, a0, a1, a1, a2, a2, a3, a3] for a tile as one 16-byte word, at a 64-byte step per tile row.
+// mstride = 32 * tile rows + 8 keeps the 16 rows of a read 16 bytes apart in the banks.
+__device__ __forceinline__ int a_slot_dup(int p, int m, int mstride) {
+  const int r = p & 15;
+  return m * mstride + ((p >> 4) << 5) + (((r & 7) >> 1) << 3) + (((r & 1) | ((r >> 3) << 1)) << 1);
 }
 
 }  // namespace exl3

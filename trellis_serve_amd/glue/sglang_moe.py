@@ -126,8 +126,8 @@ class Exl3MoEMethod(SGLANG.FusedMoEMethodBase):
             stacked[role] = (torch.stack(trs), torch.stack(suhs), torch.stack(svhs))
         if len(codebooks) != 1:
             raise NotImplementedError(f"{self.prefix}: mixed codebooks {sorted(codebooks)}")
-        if len(set(bits.values())) != 1:
-            raise NotImplementedError(f"{self.prefix}: gate / up / down bitrates differ {bits} (one K per layer)")
+        if bits["gate"] != bits["up"]:
+            raise NotImplementedError(f"{self.prefix}: gate and up bitrates differ {bits}")
         H, I = layer.exl3_hidden, layer.exl3_inter
         g, d = stacked["gate"][0], stacked["down"][0]
         if (g.shape[1] * 16, g.shape[2] * 16) != (H, I) or (d.shape[1] * 16, d.shape[2] * 16) != (I, H):
@@ -138,7 +138,7 @@ class Exl3MoEMethod(SGLANG.FusedMoEMethodBase):
             for part, tensor in zip(("trellis", "suh", "svh"), stacked[role]):
                 layer.register_buffer(f"exl3_{role}_{part}", tensor.to(dev).contiguous(), persistent=False)
         layer.exl3_codebook = CODEBOOK_ID[codebooks.pop()]
-        layer.exl3_bits = bits["gate"]
+        layer.exl3_bits = bits
         store.clear()
         del layer.exl3_store
         for w in ("w13", "w2"):
@@ -147,8 +147,8 @@ class Exl3MoEMethod(SGLANG.FusedMoEMethodBase):
         if dev.type == "cuda":
             from .. import ops
             ops.init_device(dev.index if dev.index is not None else torch.cuda.current_device())
-        logger.info("%s: %d experts, K=%d, codebook %d, stacked for exl3_moe_forward", self.prefix, E,
-                    layer.exl3_bits, layer.exl3_codebook)
+        logger.info("%s: %d experts, K gate/up %d down %d, codebook %d, stacked for exl3_moe_forward", self.prefix,
+                    E, bits["gate"], bits["down"], layer.exl3_codebook)
 
     def experts(self, layer) -> dict[str, torch.Tensor]:
         from ..ops import MOE_TENSORS

@@ -14,11 +14,6 @@ from . import _lib
 
 CODEBOOK_ID = {"3inst": 0, "mcg": 1, "mul1": 2}
 
-_workspace: dict[int, torch.Tensor] = {}
-_prefill_ws: dict[int, torch.Tensor] = {}
-_moe_ws: dict[int, torch.Tensor] = {}
-_kv_ws: dict[int, torch.Tensor] = {}
-
 
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
@@ -49,19 +44,136 @@ def _half(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device reusable scratch (split counters + fp32 split-K partials); grows, never shrinks
-    (kernels/marlin.py:24-33).  Zero-filled once at allocation: the kernels leave the counters at zero."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    cur = _workspace.get(idx)
-    if cur is None or cur.numel() < nbytes:
-        cur = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
-        _workspace[idx] = cur
-    return cur
+class WorkspaceTooSmall(RuntimeError):
+    """A call inside HIP-graph capture needs more workspace than was reserved (nothing may allocate there)."""
+
+
+class _Workspace:
+    """The per-device scratch of one kind of launch (split counters, rotated activations, fp32 partials).
+
+    A workspace only ever grows by replacement while no captured graph can hold its address.  Once it has been used
+    inside a graph capture it is never freed or replaced: a later eager call that needs more runs on a temporary
+    buffer of its own (as the reference's run does past its reserved rows, cuda/src/sglang_exl3/kernels/marlin.py:
+    86-89), and a capture that needs more raises WorkspaceTooSmall.  After `reserve_*` the workspace keeps its
+    reserved size the same way, so an engine that reserves for its largest batch at load time never allocates on the
+    serving path (cuda/src/sglang_exl3/kernels/base.py:74-76)."""
+
+    def __init__(self, kind: str, zeroed: bool):
+        self.kind, self.zeroed = kind, zeroed
+        self.buf: torch.Tensor | None = None
+        self.reserved = False   # sized by reserve_*: later calls beyond it use a temporary buffer
+        self.captured = False   # used inside a graph capture: the address must never change
+
+    def _alloc(self, nbytes: int, device: torch.device) -> torch.Tensor:
+        # counters must start at zero (every call leaves them there); the KV workspace holds only fully written data
+        make = torch.zeros if self.zeroed else torch.empty
+        return make(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        capturing = torch.cuda.is_current_stream_capturing()
+        if self.buf is not None and self.buf.numel() >= nbytes:
+            self.captured |= capturing
+            return self.buf
+        have = 0 if self.buf is None else self.buf.numel()
+        if capturing:
+            raise WorkspaceTooSmall(f"{self.kind} workspace on {device} holds {have} bytes, a call inside graph capture "
+                                    f"needs {nbytes}: call ops.reserve_{self.kind}(...) for the largest shape before "
+                                    f"capturing")
+        if self.captured or self.reserved:
+            return self._alloc(nbytes, device)   # one-off: the reserved buffer keeps its address
+        self.buf = self._alloc(nbytes, device)
+        return self.buf
+
+    def reserve(self, device: torch.device, nbytes: int) -> None:
+        if self.buf is None or self.buf.numel() < nbytes:
+            if self.captured:
+                raise WorkspaceTooSmall(f"{self.kind} workspace on {device} is held by a captured graph; reserve "
+                                        f"{nbytes} bytes before the first capture")
+            self.buf = self._alloc(nbytes, device)
+        self.reserved = True
+
+
+_KINDS = {"linear": True, "prefill": True, "moe": True, "kv": False}
+_workspaces: dict[tuple[str, int], _Workspace] = {}
+
+
+def _dev_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _ws(kind: str, device: torch.device) -> _Workspace:
+    key = (kind, _dev_index(device))
+    ws = _workspaces.get(key)
+    if ws is None:
+        ws = _workspaces[key] = _Workspace(kind, _KINDS[kind])
+    return ws
+
+
+def workspace(device: torch.device, nbytes: int, kind: str = "linear") -> torch.Tensor:
+    """The per-device workspace of `kind` ("linear", "prefill", "moe", "kv") holding at least `nbytes`."""
+    dev = torch.device("cuda", _dev_index(device))
+    return _ws(kind, dev).get(dev, nbytes)
+
+
+def release_workspaces() -> None:
+    """Drops every workspace (tests; an engine that has captured graphs must keep them)."""
+    _workspaces.clear()
+
+
+def _max_need(fn, max_rows: int) -> int:
+    """The largest workspace any row count 1..max_rows needs (split plans do not grow monotonically with rows)."""
+    return max(fn(r) for r in range(1, max(1, int(max_rows)) + 1))
+
+
+def reserve_linear(device: torch.device, max_rows: int, k: int, n_total: int, K: int) -> None:
+    """Reserves the decode-GEMV workspace for every call of up to `max_rows` rows on a group of input width k and
+    n_total output columns at bitrate K (the reference reserves its scratch at load, kernels/marlin.py:24-33)."""
+    lib = _lib.load()
+    dev = torch.device("cuda", _dev_index(device))
+    _ws("linear", dev).reserve(dev, _max_need(lambda r: lib.exl3_linear_workspace_bytes(r, k, n_total, K), max_rows))
+
+
+def reserve_prefill(device: torch.device, max_rows: int, k: int, n_total: int, nshards: int) -> None:
+    """Reserves the decode-GEMM workspace for every call of up to `max_rows` rows."""
+    lib = _lib.load()
+    dev = torch.device("cuda", _dev_index(device))
+    with torch.cuda.device(dev):   # the plan depends on the device's CU count
+        need = _max_need(lambda r: lib.exl3_prefill_workspace_bytes(r, k, n_total, nshards), max_rows)
+    _ws("prefill", dev).reserve(dev, need)
+
+
+def reserve_moe(device: torch.device, max_tokens: int, top_k: int, num_experts: int, hidden: int, inter: int,
+                K_gate_up: int, K_down: int) -> None:
+    """Reserves the MoE workspace for every call of up to `max_tokens` tokens."""
+    lib = _lib.load()
+    dev = torch.device("cuda", _dev_index(device))
+    need = _max_need(lambda t: lib.exl3_moe_workspace_bytes(t, top_k, num_experts, hidden, inter, K_gate_up,
+                                                            K_down), max_tokens)
+    _ws("moe", dev).reserve(dev, need)
+
+
+def reserve_kv(device: torch.device, max_batch: int, num_q_heads: int, num_kv_heads: int, max_pages: int) -> None:
+    """Reserves the KV decode-attention workspace for batches of up to `max_batch` sequences of `max_pages` pages."""
+    lib = _lib.load()
+    dev = torch.device("cuda", _dev_index(device))
+    _ws("kv", dev).reserve(dev, lib.exl3_kv_decode_workspace_bytes(max_batch, num_q_heads, num_kv_heads, max_pages))
 
 
 def reserve_workspace(device: torch.device, rows: int, k: int, n_total: int, K: int) -> None:
-    workspace(device, _lib.load().exl3_linear_workspace_bytes(rows, k, n_total, K))
+    """Older name of reserve_linear."""
+    reserve_linear(device, rows, k, n_total, K)
+
+
+def _check_out(out: torch.Tensor, shape: tuple, like: torch.Tensor, dtypes=(torch.float16, torch.bfloat16)) -> None:
+    """A caller-supplied output must be exactly what the kernels write: the C-ABI only sees a pointer."""
+    if tuple(out.shape) != tuple(shape):
+        raise ValueError(f"out has shape {tuple(out.shape)}, expected {tuple(shape)}")
+    if out.dtype not in dtypes:
+        raise ValueError(f"out must be one of {[str(d) for d in dtypes]}, got {out.dtype}")
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+    if out.device != like.device:
+        raise ValueError(f"out is on {out.device}, the inputs on {like.device}")
 
 
 def init_device(index: int) -> None:
@@ -122,6 +234,7 @@ def gemm_rotated(xh: torch.Tensor, trellis: torch.Tensor, codebook: int,
     rows = xh.shape[0]
     if out is None:
         out = torch.empty((rows, n), dtype=torch.float16, device=xh.device)
+    _check_out(out, (rows, n), xh, (torch.float16,))
     lib = _lib.load()
     ws = workspace(xh.device, lib.exl3_linear_workspace_bytes(rows, k, n, K))
     _lib.check(lib.exl3_gemm_rotated(xh.data_ptr(), rows, k, trellis.data_ptr(), n, K, int(codebook),
@@ -129,7 +242,7 @@ def gemm_rotated(xh: torch.Tensor, trellis: torch.Tensor, codebook: int,
     return out
 
 
-def _shards(trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor]):
+def _shards(trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor], device: torch.device):
     if not (1 <= len(trellis) <= _lib.MAX_SHARDS) or not (len(trellis) == len(suh) == len(svh)):
         raise ValueError(f"1..{_lib.MAX_SHARDS} shards with one trellis, suh and svh each")
     arr = (_lib.Exl3Shard * len(trellis))()
@@ -142,6 +255,8 @@ def _shards(trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torc
             raise ValueError("all shards of a group share the input width k and the bitrate K")
         if _half(su, "suh").numel() != k or _half(sv, "svh").numel() != n:
             raise ValueError(f"shard {i}: suh/svh sizes {su.numel()}/{sv.numel()} != {k}/{n}")
+        if not (t.device == su.device == sv.device == device):
+            raise ValueError(f"shard {i}: tensors on {t.device}/{su.device}/{sv.device}, x on {device}")
         arr[i] = _lib.Exl3Shard(t.data_ptr(), su.data_ptr(), sv.data_ptr(), n)
     return arr, k0, K0
 
@@ -152,7 +267,7 @@ def linear(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor]
     dtype (exl3_linear_marlin_multi_out, cuda/csrc/exl3_marlin.cu:507-527)."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"x must be fp16 or bf16, got {x.dtype}")
-    arr, k, K = _shards(trellis, suh, svh)
+    arr, k, K = _shards(trellis, suh, svh, x.device)
     rows2d = x.reshape(-1, x.shape[-1]).contiguous()
     if rows2d.shape[1] != k:
         raise ValueError(f"x has {rows2d.shape[1]} features, the group expects {k}")
@@ -160,6 +275,7 @@ def linear(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor]
     n_total = sum(a.n for a in arr)
     if out is None:
         out = torch.empty((rows, n_total), dtype=x.dtype, device=x.device)
+    _check_out(out, (rows, n_total), x)
     lib = _lib.load()
     ws = workspace(x.device, lib.exl3_linear_workspace_bytes(rows, k, n_total, K))
     _lib.check(lib.exl3_linear(rows2d.data_ptr(), int(x.dtype == torch.bfloat16), rows, k, arr, len(arr), K,
@@ -175,7 +291,7 @@ def linear_prefill(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch
     cuda/src/sglang_exl3/runtime/ops.py:87-95)."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"x must be fp16 or bf16, got {x.dtype}")
-    arr, k, K = _shards(trellis, suh, svh)
+    arr, k, K = _shards(trellis, suh, svh, x.device)
     rows2d = x.reshape(-1, x.shape[-1]).contiguous()
     if rows2d.shape[1] != k:
         raise ValueError(f"x has {rows2d.shape[1]} features, the group expects {k}")
@@ -183,14 +299,11 @@ def linear_prefill(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch
     n_total = sum(a.n for a in arr)
     if out is None:
         out = torch.empty((rows, n_total), dtype=x.dtype, device=x.device)
+    _check_out(out, (rows, n_total), x)
     lib = _lib.load()
-    need = lib.exl3_prefill_workspace_bytes(rows, k, n_total, len(arr))
-    idx = x.device.index if x.device.index is not None else torch.cuda.current_device()
-    ws = _prefill_ws.get(idx)
-    if ws is None or ws.numel() < need:
-        # zero-filled once: its split counters start at zero and every call leaves them there
-        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
-        _prefill_ws[idx] = ws
+    with torch.cuda.device(x.device):   # the plan depends on the device's CU count
+        need = lib.exl3_prefill_workspace_bytes(rows, k, n_total, len(arr))
+    ws = workspace(x.device, need, "prefill")
     _lib.check(lib.exl3_linear_prefill(rows2d.data_ptr(), int(x.dtype == torch.bfloat16), rows, k, arr, len(arr), K,
                                        int(codebook), out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(),
                                        ws.numel(), _stream(x.device)), "linear_prefill")
@@ -205,36 +318,46 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Ten
                 codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """Routed SiLU-gated EXL3 MoE layer (cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294).
     x fp16|bf16 [T, H]; topk_ids [T, top_k] (int32 or int64); topk_weights fp32 [T, top_k]; `experts` holds the
-    stacked tensors named in MOE_TENSORS (trellis int16 [E, k/16, n/16, 16K], scales fp16 [E, k] / [E, n])."""
+    stacked tensors named in MOE_TENSORS (trellis int16 [E, k/16, n/16, 16K], scales fp16 [E, k] / [E, n]).
+    Gate and up share one bitrate, down may have another (cuda/src/sglang_exl3/kernels/reference.py:123-149)."""
     if x.dtype not in (torch.float16, torch.bfloat16) or x.dim() != 2:
         raise ValueError("x must be a 2-D fp16/bf16 tensor")
     T, H = x.shape
-    gt, dt = experts["gate_trellis"], experts["down_trellis"]
-    if gt.dim() != 4 or dt.dim() != 4 or gt.dtype != torch.int16:
+    gt, ut, dt = experts["gate_trellis"], experts["up_trellis"], experts["down_trellis"]
+    if any(t.dim() != 4 or t.dtype != torch.int16 for t in (gt, ut, dt)):
         raise ValueError("stacked trellis tensors must be int16 [E, k/16, n/16, 16K]")
-    E, I, K = gt.shape[0], gt.shape[2] * 16, gt.shape[3] // 16
-    if gt.shape[1] * 16 != H or tuple(dt.shape[1:3]) != (I // 16, H // 16) or dt.shape[3] != 16 * K:
+    E, I = gt.shape[0], gt.shape[2] * 16
+    K_gu, K_dn = bits_of(gt), bits_of(dt)
+    if ut.shape != gt.shape:
+        raise ValueError(f"gate {tuple(gt.shape)} and up {tuple(ut.shape)} must have one shape and bitrate")
+    if gt.shape[1] * 16 != H or tuple(dt.shape[:3]) != (E, I // 16, H // 16):
         raise ValueError(f"expert shapes {tuple(gt.shape)} / {tuple(dt.shape)} do not match H = {H}")
+    sizes = {"gate_suh": H, "up_suh": H, "gate_svh": I, "up_svh": I, "down_suh": I, "down_svh": H}
     for name in MOE_TENSORS:
         t = experts[name]
-        if not (t.is_cuda and t.is_contiguous()) or t.shape[0] != E:
-            raise ValueError(f"{name} must be a contiguous CUDA tensor with {E} experts")
+        if not (t.is_cuda and t.is_contiguous()) or t.shape[0] != E or t.device != x.device:
+            raise ValueError(f"{name} must be a contiguous tensor with {E} experts on {x.device}")
+        if name in sizes and (t.dtype != torch.float16 or tuple(t.shape) != (E, sizes[name])):
+            raise ValueError(f"{name} must be fp16 [{E}, {sizes[name]}], got {t.dtype} {tuple(t.shape)}")
+    if topk_ids.dim() != 2 or topk_ids.shape[0] != T or tuple(topk_weights.shape) != tuple(topk_ids.shape):
+        raise ValueError(f"topk_ids {tuple(topk_ids.shape)} and topk_weights {tuple(topk_weights.shape)} must both be "
+                         f"[{T}, top_k]")
+    if topk_ids.dtype not in (torch.int32, torch.int64) or topk_ids.device != x.device \
+            or topk_weights.device != x.device:
+        raise ValueError("topk_ids must be int32/int64 and both routing tensors on x's device")
     top_k = topk_ids.shape[1]
     ids = topk_ids.to(torch.int32).contiguous()
     w = topk_weights.to(torch.float32).contiguous()
     if out is None:
         out = torch.empty((T, H), dtype=x.dtype, device=x.device)
+    _check_out(out, (T, H), x)
     lib = _lib.load()
-    need = lib.exl3_moe_workspace_bytes(T, top_k, E, H, I, K)
-    idx = x.device.index if x.device.index is not None else torch.cuda.current_device()
-    ws = _moe_ws.get(idx)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=x.device)
-        _moe_ws[idx] = ws
+    ws = workspace(x.device, lib.exl3_moe_workspace_bytes(T, top_k, E, H, I, K_gu, K_dn), "moe")
     wts = _lib.Exl3MoeWeights(*[experts[n].data_ptr() for n in MOE_TENSORS])
     _lib.check(lib.exl3_moe_forward(x.contiguous().data_ptr(), int(x.dtype == torch.bfloat16), T, H, ids.data_ptr(),
-                                    w.data_ptr(), top_k, E, I, ctypes.byref(wts), K, int(codebook), out.data_ptr(),
-                                    int(out.dtype == torch.bfloat16), ws.data_ptr(), ws.numel(), _stream(x.device)),
+                                    w.data_ptr(), top_k, E, I, ctypes.byref(wts), K_gu, K_dn, int(codebook),
+                                    out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(), ws.numel(),
+                                    _stream(x.device)),
                "moe_forward")
     return out
 
@@ -266,20 +389,16 @@ def kv_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     if seq_lens.dtype != torch.int32 or tuple(seq_lens.shape) != (B,):
         raise ValueError("seq_lens must be int32 [B]")
     tensors = (q, k_cache, v_cache, k_scale, v_scale, page_table, seq_lens)
-    if not all(t.is_cuda and t.is_contiguous() for t in tensors):
-        raise ValueError("all inputs must be contiguous CUDA tensors")
+    if not all(t.is_cuda and t.is_contiguous() and t.device == q.device for t in tensors):
+        raise ValueError("all inputs must be contiguous CUDA tensors on one device")
     if sm_scale is None:
         sm_scale = D ** -0.5
     if out is None:
         out = torch.empty((B, Hq, D), dtype=torch.float16, device=q.device)
+    _check_out(out, (B, Hq, D), q, (torch.float16,))
     lib = _lib.load()
     max_pages = page_table.shape[1]
-    need = lib.exl3_kv_decode_workspace_bytes(B, Hq, Hkv, max_pages)
-    idx = q.device.index if q.device.index is not None else torch.cuda.current_device()
-    ws = _kv_ws.get(idx)
-    if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)
-        _kv_ws[idx] = ws
+    ws = workspace(q.device, lib.exl3_kv_decode_workspace_bytes(B, Hq, Hkv, max_pages), "kv")
     _lib.check(lib.exl3_kv_decode_attention(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_scale.data_ptr(),
                                             v_scale.data_ptr(), P, page_table.data_ptr(), max_pages,
                                             seq_lens.data_ptr(), B, Hq, Hkv, D, page, int(bits), float(sm_scale),
