@@ -94,7 +94,45 @@ def test_gemm_rotated_one_hot_readout_is_exact(coracle, K, cb):
     np.testing.assert_array_equal(w.view(np.uint16), c_reconstruct(coracle, tr, K, cb).view(np.uint16))
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 17])
+@pytest.mark.parametrize("K", (2, 3, 4))
+@pytest.mark.parametrize("cb", CBS)
+def test_one_hot_readout_through_the_split_k_gemv_is_exact(coracle, K, cb):
+    """The decode-GEMV (split-K: every k split of a 128-column block writes fp32 partials, the last arrival sums
+    them) read back with one-hot rows: each row of W_inner comes back bit for bit, 4 rows per call and once with a
+    single row (the two-halves MFMA path below 8 rows).  1280 x 16384 has 10 k blocks and 128 column blocks."""
+    rng = np.random.default_rng(2500 + 10 * K + cb)
+    k, n = 1280, 16384
+    tr = _trellis(rng, k, n, K)
+    dtr = _dev(tr)
+    ref = c_reconstruct(coracle, tr, K, cb).view(np.uint16)
+    eye = torch.eye(k, dtype=torch.float16, device="cuda")
+    got = np.concatenate([_ops().gemm_rotated(eye[r0:r0 + 4].contiguous(), dtr, cb).cpu().numpy()
+                          for r0 in range(0, k, 4)])
+    np.testing.assert_array_equal(got.view(np.uint16), ref)
+    one = _ops().gemm_rotated(eye[37:38].contiguous(), dtr, cb).cpu().numpy()
+    np.testing.assert_array_equal(one.view(np.uint16), ref[37:38])
+
+
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("cb", CBS)
+def test_gemv_shards_of_uneven_widths(coracle, M, cb):
+    """A 3-shard group of uneven widths (23, 10 and 20 column blocks): column blocks of different shards in one launch
+    rotate their activations with their own suh and their outputs with their own svh.  Against the float64 oracle."""
+    rng = np.random.default_rng(3500 + 10 * M + cb)
+    k, ns, K = 4096, (2944, 1280, 2560), 3
+    trs = [_trellis(rng, k, n, K) for n in ns]
+    suhs = [_signs(rng, k) for _ in ns]
+    svhs = [_signs(rng, n) for n in ns]
+    x = (rng.standard_normal((M, k)) * 0.5).astype(np.float16)
+    y = _ops().linear(_dev(x), [_dev(t) for t in trs], [_dev(s) for s in suhs], [_dev(s) for s in svhs],
+                      cb).cpu().numpy()
+    ref = np.concatenate([orc.linear_forward(x, t, a, b, K, cb, w_inner=c_reconstruct(coracle, t, K, cb),
+                                             dtype=np.float64) for t, a, b in zip(trs, suhs, svhs)], axis=1)
+    nrel, mrel = _errs(y, ref)
+    assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 17])
 @pytest.mark.parametrize("K,cb", [(2, 1), (3, 1), (4, 0), (5, 2), (6, 1), (8, 0)])
 def test_linear_matches_float64_oracle(coracle, M, K, cb):
     rng = np.random.default_rng(3000 + 100 * M + 10 * K + cb)
