@@ -93,6 +93,19 @@ int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* sh
 int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook, void* out,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free form of exl3_linear.  No counterpart in the reference: it is for callers that cannot allocate or
+ * pass device memory of their own (code under HIP-graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as exl3_linear without the workspace: the split counters and fp32
+ * partials live in a scratch array of EXL3_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * until the process ends.  It calls no allocating routine.  A call whose exl3_linear_workspace_bytes exceeds the
+ * scratch returns EXL3_ERR_INVALID and launches nothing.  All calls on one GPU share its scratch: calls that overlap
+ * in time on one GPU (several streams, several host threads without ordering) race and give wrong results; calls
+ * ordered on one stream are safe, and each leaves the counters at zero for the next. */
+#define EXL3_NOALLOC_SCRATCH_BYTES (32u << 20)
+size_t exl3_linear_noalloc_max_bytes(void);
+int exl3_linear_noalloc(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards, int K,
+                        int codebook, void* y, int y_bf16, void* stream);
+
 /* ---- prefill decode-GEMM (subsystem 3) ------------------------------------------------------------------------ */
 /* Workspace bytes of exl3_linear_prefill for `rows` rows of a group with input width k, n_total output columns and
  * nshards shards: EXL3_WORKSPACE_COUNTER_BYTES of split counters (zero before the first use; every call leaves them

@@ -11,6 +11,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "exl3_api.hpp"
 #include "exl3_device.hpp"
@@ -556,6 +557,42 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
 
 using namespace exl3;
 
+// ---- scratch of the allocation-free entry point ----------------------------------------------------------------
+// exl3_linear_noalloc runs the GEMV on this file-scope array instead of a caller's workspace: the same layout (the
+// counter region, then the fp32 partials and rotated rows).  Every GPU the library runs on holds its own copy at its
+// own address for the life of the process.  In host code `scratch` names a host-side stand-in, never the device
+// memory: kernels and copies take the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) uint8_t scratch[EXL3_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The current device's scratch address, looked up (and its counter region cleared by a fill kernel on `st`) on the
+// first call for that device.  Every GEMV call leaves its counters at zero again, so clearing once is enough.
+static int scratch_of_current_device(hipStream_t st, void** out) {
+  int dev = 0;
+  EXL3_CHECK_HIP(hipGetDevice(&dev));
+  EXL3_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "exl3_linear_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    EXL3_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    EXL3_CHECK_ARG(p != nullptr, "exl3_linear_noalloc: no device address for the scratch array");
+    const int words = (int)(kCounterBytes / 4);
+    zero_words_kernel<<<dim3((unsigned)((words + 255) / 256)), 256, 0, st>>>(static_cast<uint32_t*>(p), words);
+    EXL3_CHECK_LAUNCH();
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return EXL3_OK;
+}
+
 extern "C" int exl3_reconstruct(const void* trellis, int k, int n, int K, int codebook, void* w_out, void* stream) {
   EXL3_CHECK_ARG(trellis && w_out, "exl3_reconstruct: null pointer");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_reconstruct: K = %d / codebook = %d", K, codebook);
@@ -650,3 +687,23 @@ extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* tr
   return launch_gemv(sa, xh, false, false, rows, k, K, codebook, n, workspace, out, false, as_stream(stream));
 }
 
+extern "C" size_t exl3_linear_noalloc_max_bytes(void) { return EXL3_NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int exl3_linear_noalloc(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host,
+                                   int nshards, int K, int codebook, void* y, int y_bf16, void* stream) {
+  EXL3_CHECK_ARG(x && y, "exl3_linear_noalloc: null x / y");
+  EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_linear_noalloc: K = %d / codebook = %d", K, codebook);
+  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_linear_noalloc: rows = %d, k = %d", rows, k);
+  ShardArgs sa;
+  int n_total = 0;
+  if (int rc = build_shards(shards_host, nshards, k, K, &sa, &n_total)) return rc;
+  if (rows == 0) return EXL3_OK;
+  const size_t need = exl3_linear_workspace_bytes(rows, k, n_total, K);
+  EXL3_CHECK_ARG(need <= (size_t)EXL3_NOALLOC_SCRATCH_BYTES,
+                 "exl3_linear_noalloc: %d rows of %d -> %d need %zu bytes of scratch, the library holds %zu; use "
+                 "exl3_linear with a workspace", rows, k, n_total, need, (size_t)EXL3_NOALLOC_SCRATCH_BYTES);
+  hipStream_t st = as_stream(stream);
+  void* ws = nullptr;
+  if (int rc = scratch_of_current_device(st, &ws)) return rc;
+  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, ws, y, y_bf16 != 0, st);
+}
