@@ -16,6 +16,8 @@ from trellis_serve_amd.glue.sglang_config import Exl3Config
 from trellis_serve_amd.glue.sglang_linear import Exl3LinearMethod
 from trellis_serve_amd.glue.sglang_moe import Exl3MoEMethod
 from trellis_serve_amd.glue import vllm_plugin
+from trellis_serve_amd.glue.index import CheckpointIndex, module_key
+from trellis_serve_amd.glue.stash import MatrixInfo, TensorStash, shard_partitions
 
 SG = engine.SGLANG
 L0 = "model.language_model.layers.0"
@@ -67,7 +69,7 @@ def test_config_routes_modules(ckpt):
     assert isinstance(m, Exl3LinearMethod) and [i[:4] for i in m.infos] == [(256, 256, 6, "mcg"), (256, 128, 6, "mcg"),
                                                                              (256, 128, 6, "mcg")]
     assert isinstance(cfg.get_quant_method(SG.LinearBase(), "model.layers.0.self_attn.o_proj"), Exl3LinearMethod)
-    assert cfg.lookup("model.layers.0.o_proj") is not None        # `.self_attn.` dropped
+    assert cfg.index.find("model.layers.0.o_proj") is not None        # `.self_attn.` dropped
     assert isinstance(cfg.get_quant_method(SG.LinearBase(), "model.layers.0.mlp.shared_expert_gate"),
                       SG.UnquantizedLinearMethod)
     head = cfg.get_quant_method(SG.ParallelLMHead(), "lm_head")
@@ -85,7 +87,7 @@ def test_linear_loading_and_validation(ckpt):
     assert layer.exl3_count == 3 and layer.exl3_widths == [256, 128, 128] and layer.exl3_runs == [(0, 3)]
     assert layer.exl3_codebooks == [1, 1, 1] and layer.exl3_bits == [3, 3, 3]
     np.testing.assert_array_equal(layer.exl3_trellis_1.cpu().numpy(), tensors[f"{L0}.self_attn.k_proj.trellis"])
-    assert not hasattr(layer, "trellis") and not hasattr(layer, "exl3_shards")
+    assert not hasattr(layer, "trellis") and not hasattr(layer, "exl3_stash")
     # legacy packed signs become the +-1 vectors
     o, om = _linear_layer(cfg, "model.layers.0.self_attn.o_proj", [256], 256)
     _feed(o, tensors, f"{L0}.self_attn.o_proj", None)
@@ -106,14 +108,14 @@ def test_linear_errors(ckpt):
     cfg = _config(path)
     layer, method = _linear_layer(cfg, "model.layers.0.mlp.gate_up_proj", [384, 384], 256)
     _feed(layer, tensors, f"{L0}.mlp.gate_proj", 0)
-    with pytest.raises(ValueError, match="loaded twice"):
+    with pytest.raises(ValueError, match="a second tensor for shard"):
         _feed(layer, tensors, f"{L0}.mlp.gate_proj", 0)
     with pytest.raises(ValueError, match="expected 2 EXL3 matrices"):
         method.process_weights_after_loading(layer)
     layer, method = _linear_layer(cfg, "model.layers.0.mlp.gate_up_proj", [384, 384], 256)
     _feed(layer, tensors, f"{L0}.mlp.gate_proj", 0)
     _feed(layer, tensors, f"{L0}.mlp.down_proj", 1)       # wrong matrix for shard 1
-    with pytest.raises(ValueError, match="does not match the header scan"):
+    with pytest.raises(ValueError, match="the checkpoint header declares"):
         method.process_weights_after_loading(layer)
     with pytest.raises(NotImplementedError, match="tensor-parallel"):
         Exl3LinearMethod("x", [(256, 256, 6, "mcg", False, False)]).create_weights(
@@ -122,7 +124,7 @@ def test_linear_errors(ckpt):
         Exl3LinearMethod("x", [(256, 256, 6, "mcg", True, False)]).create_weights(
             SG.LinearBase(), 256, [256], 256, 256, torch.float16)
     with pytest.raises(ValueError, match="mixes EXL3 and unquantized"):
-        cfg.modules.pop(f"{L0}.mlp.up_proj")
+        cfg.index.forget(f"{L0}.mlp.up_proj")
         cfg.get_quant_method(SG.LinearBase(), "model.layers.0.mlp.gate_up_proj")
 
 
@@ -189,7 +191,8 @@ def _vllm_qkv(path, tensors):
 def test_vllm_method(ckpt):
     path, tensors = ckpt
     layer, method = _vllm_qkv(path, tensors)
-    assert method.K == 3 and layer.exl3_cb == 1 and layer.exl3_count == 3 and layer.exl3_runs == [(0, 3)]
+    assert layer.exl3_codebooks == [1, 1, 1] and layer.exl3_bits == [3, 3, 3] and layer.exl3_count == 3
+    assert layer.exl3_runs == [(0, 3)]
     for i, sid in enumerate("qkv"):
         key = f"{L0}.self_attn.{sid}_proj"
         np.testing.assert_array_equal(getattr(layer, f"exl3_trellis_{i}").cpu().numpy(), tensors[f"{key}.trellis"])
@@ -197,11 +200,99 @@ def test_vllm_method(ckpt):
         assert getattr(layer, f"exl3_trellis_{i}").is_contiguous()
     cfg = vllm_plugin.Exl3Config.from_config({})
     cfg.maybe_update_config(path)
-    assert cfg.storage["lm_head"] == (4, "mul1") and cfg.storage["layers.0.self_attn.q_proj"] == (3, "mcg")
+    assert cfg.index.find("lm_head")[:4] == (256, 512, 8, "mul1")
+    assert cfg.index.find("language_model.model.layers.0.self_attn.q_proj")[:4] == (256, 256, 6, "mcg")
     assert isinstance(cfg.get_quant_method(engine.VLLM.LinearBase(), "model.layers.0.mlp.foo_proj"),
                       engine.VLLM.UnquantizedLinearMethod)
-    assert vllm_plugin.module_key("language_model.model.layers.3.mlp.gate_proj") == "layers.3.mlp.gate_proj"
-    assert vllm_plugin.module_key("model.mtp.layers.0.mlp.up_proj") == "mtp.layers.0.mlp.up_proj"
+
+
+def test_vllm_declared_format_without_a_local_checkpoint(ckpt):
+    """A model directory that is not local: the declared bitrate decides which linears are EXL3 and is checked
+    against what arrives; shapes follow the layer, the codebook the checkpoint's marker tensors."""
+    path, tensors = ckpt
+    cfg = vllm_plugin.Exl3Config.from_config({"bits": 3, "head_bits": 4, "codebook": "mcg"})
+    cfg.maybe_update_config("org/not-a-local-dir")
+    assert cfg.index is None
+    assert cfg.get_quant_method(engine.VLLM.LinearBase(), "model.layers.0.linear_attn.in_proj_ba") is not None
+    assert isinstance(cfg.get_quant_method(engine.VLLM.LinearBase(), "model.layers.0.linear_attn.in_proj_ba"),
+                      engine.VLLM.UnquantizedLinearMethod)
+    assert isinstance(cfg.get_quant_method(engine.VLLM.LinearBase(), "model.visual.blocks.0.attn.qkv"),
+                      engine.VLLM.UnquantizedLinearMethod)
+    assert cfg.get_quant_method(engine.VLLM.ParallelLMHead(), "lm_head").declared_bits == 4
+    layer = engine.VLLM.LinearBase()
+    method = cfg.get_quant_method(layer, "model.layers.0.self_attn.qkv_proj")
+    assert method.declared_bits == 3 and method.infos is None
+    method.create_weights(layer, 256, [256, 128, 128], 256, 512, torch.float16)
+    for sid in "qkv":
+        key = f"{L0}.self_attn.{sid}_proj"
+        for suffix in ("trellis", "suh", "svh", "mcg"):
+            p = getattr(layer, suffix)
+            p.weight_loader(p, torch.from_numpy(np.array(tensors[f"{key}.{suffix}"])), sid)
+    method.process_weights_after_loading(layer)
+    assert layer.exl3_codebooks == [1, 1, 1] and layer.exl3_widths == [256, 128, 128]
+    # a shard at another bitrate than declared
+    cfg4 = vllm_plugin.Exl3Config.from_config({"bits": 4})
+    layer = engine.VLLM.LinearBase()
+    method = cfg4.get_quant_method(layer, "model.layers.0.self_attn.o_proj")
+    method.create_weights(layer, 256, [256], 256, 256, torch.float16)
+    for suffix in ("trellis", "su", "sv", "mcg"):
+        p = getattr(layer, suffix)
+        p.weight_loader(p, torch.from_numpy(np.array(tensors[f"{L0}.self_attn.o_proj.{suffix}"])))
+    with pytest.raises(ValueError, match="declares K=4"):
+        method.process_weights_after_loading(layer)
+
+
+def test_checkpoint_index_spellings_and_experts():
+    mcg3 = MatrixInfo(256, 256, 6, "mcg")
+    idx = CheckpointIndex({
+        "model.language_model.layers.2.self_attn.q_proj": mcg3,
+        "model.language_model.layers.2.mlp.experts.0.gate_proj": mcg3,
+        "model.language_model.layers.2.mlp.experts.0.down_proj": mcg3,
+        "model.language_model.layers.2.mlp.experts.11.up_proj": mcg3,
+        "mtp.layers.0.mlp.down_proj": mcg3,
+        "lm_head": MatrixInfo(256, 512, 8, "mul1"),
+    })
+    for spelling in ("model.language_model.layers.2.self_attn.q_proj", "model.layers.2.self_attn.q_proj",
+                     "model.layers.2.q_proj", "language_model.model.layers.2.self_attn.q_proj"):
+        assert idx.find(spelling) == mcg3, spelling
+    assert module_key("language_model.model.layers.3.mlp.gate_proj") == "layers.3.mlp.gate_proj"
+    assert module_key("model.mtp.layers.0.mlp.up_proj") == "mtp.layers.0.mlp.up_proj"
+    assert idx.find("model.layers.0.mlp.down_proj") == mcg3            # a draft's layer 0 is the checkpoint's mtp
+    assert idx.find("model.layers.3.q_proj") is None and "lm_head" in idx
+    assert idx.find("model.visual.layers.2.q_proj") is None             # towers keep their own prefix
+    assert idx.experts("model.layers.2.mlp.experts") == {("gate", 0): mcg3, ("down", 0): mcg3, ("up", 11): mcg3}
+    assert idx.linear("model.layers.2.mlp.gate_up_proj") is None
+    with pytest.raises(ValueError, match="mixes EXL3 and unquantized"):
+        idx.linear("model.layers.2.self_attn.qkv_proj")
+    assert idx.linear("model.layers.2.qkv_proj", {"qkv_proj": ["q_proj"]}) == [mcg3]   # the engine's own map
+    with pytest.raises(ValueError, match="same module"):
+        CheckpointIndex({"model.layers.0.q_proj": mcg3, "model.language_model.layers.0.self_attn.q_proj": mcg3})
+    bad = CheckpointIndex({"model.layers.1.mlp.experts.0.w9": mcg3})
+    with pytest.raises(ValueError, match="unexpected EXL3 matrix"):
+        bad.experts("model.layers.1.mlp.experts")
+
+
+def test_stash_keys_and_legacy_signs():
+    assert shard_partitions(None) == () and shard_partitions("k") == (1,) and shard_partitions([0, "v"]) == (0, 2)
+    st = TensorStash("blk", "cpu")
+    tr = torch.zeros((16, 8, 48), dtype=torch.int16)
+    st.put((1,), "trellis", tr)
+    with pytest.raises(ValueError, match="a second tensor"):
+        st.put((1,), "trellis", tr)
+    with pytest.raises(ValueError, match="not an EXL3 checkpoint suffix"):
+        st.put((1,), "weight", tr)
+    with pytest.raises(ValueError, match="without suh/svh"):
+        st.matrix((1,))
+    words = torch.tensor([0x0001, -0x8000], dtype=torch.int16)       # bit 0 of word 0, bit 15 of word 1
+    st.put((1,), "su", torch.zeros(16, dtype=torch.int16))
+    st.put((1,), "sv", torch.cat([words, torch.zeros(6, dtype=torch.int16)]))
+    st.put((1,), "mul1", torch.zeros((), dtype=torch.int32))
+    m = st.matrix((1,), MatrixInfo(256, 128, 6, "mul1"))
+    assert m.codebook_id == 2 and m.bits == 3 and m.suh.dtype == torch.float16 and bool((m.suh == 1).all())
+    sv = m.svh.tolist()
+    assert sv[0] == -1 and sv[31] == -1 and sv.count(-1) == 2
+    with pytest.raises(ValueError, match="the checkpoint header declares"):
+        st.matrix((1,), MatrixInfo(256, 128, 8, "mul1"))
 
 
 def test_plugin_registration():
