@@ -127,7 +127,148 @@ def _cpu_threads() -> int:
     return max(1, min(16, n))
 
 
-def cpu_baseline(seconds_target: float = 12.0) -> dict:
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_s(fn, runs: int) -> float:
+    times = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    return float(np.median(times))
+
+
+MOE_SHAPE = (128, 2048, 768, 3, 8)  # E, H, I, K, top_k
+KV_SHAPE = (16, 40, 8, 128)         # B, Hq, Hkv, head_dim
+
+
+def cpu_table(runs: int = 3, sample_tiles: int = 8192) -> dict:
+    """The CPU baseline of BASELINE.md section 3: the reference's CPU path (trellis_core reference.py:80-153) restated
+    in torch (oracle/torch_cpu.py) on the host's cores, median of `runs` runs, decode and matmul timed apart:
+      C1  4096 x 4096, K = 4, 3INST, M = 1: the whole path (all 65536 tiles decoded);
+      C2  the 27B layer set at M = 1 (K = 3, MCG), per layer, each source matrix as the reference runs it;
+      C3  5120 -> 17408 at M = 512, one K per codebook (K = 3 MCG, K = 2 3INST, K = 4 MUL1);
+      C4  the MoE layer at T = 1 (8 experts x gate, up, down), SiLU-gated;
+      C5  quantized-KV attention at 4k context: closed-form dequant of the pages + fp32 attention, 8 and 4 bits.
+    Decode of C2-C4 is timed on the first `sample_tiles` tiles of each matrix (decode time is linear in tiles) and
+    scaled to the whole matrix; matmuls (fp32 Hadamards + GEMM) run at full size on a same-shaped fp32 W."""
+    import torch
+
+    from oracle import torch_cpu as tc
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(7)
+
+    def trellis(tiles, K):
+        return torch.randint(-32768, 32768, (1, tiles, 16 * K), dtype=torch.int16, generator=g)
+
+    def signs(n):
+        return (torch.randint(0, 2, (n,), generator=g) * 2 - 1).half()
+
+    def decode_s(k, n, K, cb, full=False):
+        tiles = (k // 16) * (n // 16)
+        take = tiles if full else min(tiles, sample_tiles)
+        tr = trellis(take, K)
+        return _median_s(lambda: tc.reconstruct_inner(tr, K, cb), runs) * tiles / take
+
+    def matmul_s(M, k, n):
+        w, x, suh, svh = torch.randn((k, n), generator=g), torch.randn((M, k), generator=g), signs(k), signs(n)
+        return _median_s(lambda: tc.linear_from_inner(x, w, suh, svh), runs)
+
+    def entry(dec, mm, nbytes=None, flops=None):
+        e = {"decode_us": round(dec * 1e6, 1), "matmul_us": round(mm * 1e6, 1), "total_us": round((dec + mm) * 1e6, 1)}
+        if nbytes is not None:
+            e["GB/s"] = round(nbytes / (dec + mm) / 1e9, 4)
+        if flops is not None:
+            e["TFLOPS"] = round(flops / (dec + mm) / 1e12, 5)
+        return e
+
+    t0 = time.perf_counter()
+    table = {}
+    # C1: the real pipeline on one matrix, parity-checked against the numpy oracle
+    from oracle import exl3_oracle as orc
+    tr = torch.randint(-32768, 32768, (256, 256, 64), dtype=torch.int16, generator=g)
+    suh, svh, x = signs(4096), signs(4096), torch.randn((1, 4096), generator=g).half()
+    w_inner = tc.reconstruct_inner(tr, 4, 0)
+    y = tc.linear_from_inner(x, w_inner, suh, svh).numpy()
+    ref = orc.linear_forward(x.numpy(), tr.numpy(), suh.numpy(), svh.numpy(), 4, 0, w_inner=w_inner.numpy())
+    rel = float(np.linalg.norm(y - ref) / np.linalg.norm(ref))
+    assert rel < 1e-5, f"torch CPU path disagrees with the oracle: {rel}"
+    dec = _median_s(lambda: tc.reconstruct_inner(tr, 4, 0), runs)
+    mm = _median_s(lambda: tc.linear_from_inner(x, w_inner, suh, svh), runs)
+    table["C1_4096_K4_3inst_M1"] = entry(dec, mm, alg_bytes(4096, [4096], 1, 4))
+    # C2: the layer set at M = 1
+    per_layer, tot_dec, tot_mm = {}, 0.0, 0.0
+    for name, (k, ns) in LAYERS.items():
+        dec = sum(decode_s(k, n, K_BITS, CODEBOOK) for n in ns)
+        mm = sum(matmul_s(1, k, n) for n in ns)
+        per_layer[name] = entry(dec, mm)
+        tot_dec, tot_mm = tot_dec + dec, tot_mm + mm
+    c2_bytes = sum(alg_bytes(k, ns, 1, K_BITS) for k, ns in LAYERS.values())
+    table["C2_layer_set_M1"] = dict(entry(tot_dec, tot_mm, c2_bytes), per_layer=per_layer)
+    # C3: M = 512, one K per codebook; the matmul does not depend on the codebook
+    mm = matmul_s(512, 5120, 17408)
+    for K, cb, tag in ((3, 1, "K3_mcg"), (2, 0, "K2_3inst"), (4, 2, "K4_mul1")):
+        table[f"C3_5120x17408_{tag}_M512"] = entry(decode_s(5120, 17408, K, cb), mm, flops=2 * 512 * 5120 * 17408)
+    # C4: the MoE layer at one token: 8 experts, each gate and up (H -> I), SiLU(g) * u, down (I -> H)
+    E, H, I, K, top_k = MOE_SHAPE
+    dec = top_k * (2 * decode_s(H, I, K, CODEBOOK) + decode_s(I, H, K, CODEBOOK))
+    ws = [(torch.randn((H, I), generator=g), torch.randn((H, I), generator=g), torch.randn((I, H), generator=g))
+          for _ in range(top_k)]
+    xs, sH, sI = torch.randn((1, H), generator=g), signs(H), signs(I)
+
+    def moe_token():
+        y = torch.zeros((1, H))
+        for wg, wu, wd in ws:
+            h = torch.nn.functional.silu(tc.linear_from_inner(xs, wg, sH, sI)) * tc.linear_from_inner(xs, wu, sH, sI)
+            y += tc.linear_from_inner(h, wd, sI, sH) / top_k
+        return y
+    moe_bytes = top_k * (2 * H * I + I * H) * K // 8
+    table["C4_moe_T1"] = entry(dec, _median_s(moe_token, runs), moe_bytes)
+    # C5: 4k context, batch 16, 40 / 8 heads
+    B, Hq, Hkv, D = KV_SHAPE
+    L = 4096
+    npg = L // 16
+    P = B * npg
+    for bits in (8, 4):
+        row = D if bits == 8 else D // 2
+        kc = torch.randint(-128, 128, (P, Hkv, 16, row), dtype=torch.int8, generator=g)
+        vc = torch.randint(-128, 128, (P, Hkv, 16, row), dtype=torch.int8, generator=g)
+        ks, vs = torch.rand((P, Hkv), generator=g).half(), torch.rand((P, Hkv), generator=g).half()
+        table_pages = torch.randperm(P, generator=g).to(torch.int32).view(B, npg)
+        q = torch.randn((B, Hq, D), generator=g).half()
+        dec = _median_s(lambda: (tc.kv_dequant(kc, ks, bits), tc.kv_dequant(vc, vs, bits)), runs)
+        kd, vd = tc.kv_dequant(kc, ks, bits), tc.kv_dequant(vc, vs, bits)
+        att = _median_s(lambda: tc.decode_attention(q, kd, vd, table_pages, D ** -0.5), runs)
+        nbytes = 2 * B * Hkv * L * row + 2 * 2 * P * Hkv + 4 * B * npg + 2 * 2 * B * Hq * D
+        table[f"C5_L4k_{bits}bit_B16"] = entry(dec, att, nbytes)
+        del kc, vc, kd, vd
+    c2 = table["C2_layer_set_M1"]
+    return {"value": c2["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"trellis_core's CPU path (reference.py:80-153) restated in torch, {threads} threads, median of "
+                      f"{runs} runs: C2 layer set at M = 1, decode of each matrix timed on its first {sample_tiles} "
+                      f"tiles and scaled, fp32 Hadamards + GEMV at full size; C1 parity vs the numpy oracle "
+                      f"{rel:.1e}",
+            "cpu_model": _cpu_model(), "torch": torch.__version__, "runs": runs,
+            "wall_s": round(time.perf_counter() - t0, 1), "table": table}
+
+
+def cpu_baseline() -> dict:
+    out = cpu_table()
+    out["c_restatement"] = cpu_c_restatement()
+    return out
+
+
+def cpu_c_restatement(seconds_target: float = 6.0) -> dict:
     """The oracle's decode + matmul on the host cores (trellis_core's CPU path restated: reference.py:102-153): the
     o_proj linear (6144 -> 5120, K = 3, MCG) at M = 1.  The k range is cut into one slice of tile rows per thread;
     each thread decodes its slice with the C restatement (oracle/exl3_oracle.c, ctypes releases the GIL) and multiplies
@@ -180,8 +321,8 @@ def cpu_baseline(seconds_target: float = 12.0) -> dict:
             reps += 1
     per = t_total / reps
     b = alg_bytes(k, [n], 1, K_BITS)
-    return {"value": round(b / per / 1e9, 4), "unit": "GB/s", "cores": nt, "kind": "port",
-            "sample": f"oracle decode (C restatement) + fp32 matmul of o_proj 6144->5120 K=3 MCG M=1 over {nt} "
+    return {"GB/s": round(b / per / 1e9, 4), "threads": nt,
+            "what": f"oracle decode (C restatement) + fp32 matmul of o_proj 6144->5120 K=3 MCG M=1 over {nt} "
                       f"threads (k cut in {nt} slices), {reps} reps, {per * 1e3:.1f} ms each; agrees with the numpy "
                       f"oracle to {rel:.1e}"}
 

@@ -299,3 +299,47 @@ def test_planted_double_rounding_in_mul1_is_caught(golden):
     two_roundings = (h * np.float16(orc._f16_from_bits(0x1EEE))).astype(np.float16) + orc._f16_from_bits(0xC931)
     assert hashlib.sha256(two_roundings.astype(np.float16).view(np.uint16).tobytes()).digest() != \
         golden["lut_sha256_cb2"].tobytes()
+
+
+# ---- the torch CPU restatement timed as the CPU baseline ---------------------------------------------------------
+
+@pytest.mark.parametrize("K", KS)
+@pytest.mark.parametrize("cb", CBS)
+def test_torch_cpu_reconstruct_matches_reference(golden, K, cb):
+    import torch
+    from oracle import torch_cpu
+    tr = torch.from_numpy(golden[f"recon_in_K{K}_cb{cb}"])
+    w = torch_cpu.reconstruct_inner(tr, K, cb, chunk=3)   # a chunk that does not divide the tile count
+    np.testing.assert_array_equal(w.numpy().view(np.uint16), golden[f"recon_out_K{K}_cb{cb}"])
+
+
+@pytest.mark.parametrize("tag", ["lin_a", "lin_b"])
+def test_torch_cpu_linear_forward_matches_reference(golden, tag):
+    import torch
+    from oracle import torch_cpu
+    k, n, K, cb = golden[f"{tag}_dims"].tolist()
+    args = [torch.from_numpy(golden[f"{tag}_{p}"]) for p in ("x", "trellis", "suh", "svh")]
+    y = torch_cpu.linear_forward(*args, K, cb).numpy()
+    ref = golden[f"{tag}_y"]
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_torch_cpu_kv_attention_matches_oracle(bits):
+    import torch
+    from oracle import torch_cpu
+    rng = np.random.default_rng(bits)
+    B, Hq, Hkv, D, npg = 3, 8, 2, 128, 5
+    P = B * npg
+    kq, ks = orc.kv_quantize(rng.standard_normal((P, Hkv, 16, D)).astype(np.float16), bits)
+    vq, vs = orc.kv_quantize(rng.standard_normal((P, Hkv, 16, D)).astype(np.float16), bits)
+    if bits == 4:
+        kq, vq = orc.kv_pack4(kq), orc.kv_pack4(vq)
+    table = rng.permutation(P).astype(np.int32).reshape(B, npg)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float16)
+    ref = orc.kv_decode_attention(q, kq, vq, ks, vs, table, np.full(B, 16 * npg, np.int32), bits, 0.088)
+    T = torch.from_numpy
+    k = torch_cpu.kv_dequant(T(kq.view(np.int8)), T(ks), bits)
+    v = torch_cpu.kv_dequant(T(vq.view(np.int8)), T(vs), bits)
+    got = torch_cpu.decode_attention(T(q), k, v, T(table), 0.088).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
