@@ -49,10 +49,10 @@ C2_LAYERS = {"qkv": (5120, [6144, 1024, 1024]), "o": (6144, [5120]), "gate_up": 
              "down": (17408, [5120])}
 
 
-@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("M", [1, 4, 16])
 @pytest.mark.parametrize("name", list(C2_LAYERS))
 def test_gemv_c2_layer_set_shapes(name, M):
-    """the four fused K = 3 MCG linears of the 27B-class layer set at M = 1 and 16."""
+    """the four fused K = 3 MCG linears of the 27B-class layer set at M = 1, 4 and 16."""
     g = torch.Generator(device="cpu").manual_seed(100 + M)
     k, ns = C2_LAYERS[name]
     trs, suhs, svhs = _layer(g, k, ns, 3)
@@ -60,7 +60,8 @@ def test_gemv_c2_layer_set_shapes(name, M):
     _check(_ops().linear(x, trs, suhs, svhs, 1), _reference(x, trs, suhs, svhs, 1))
 
 
-@pytest.mark.parametrize("K,cb,M", [(3, 1, 2048), (2, 0, 512), (8, 2, 512)])
+@pytest.mark.parametrize("K,cb,M", [(3, 1, 2048), (2, 0, 512), (8, 2, 512), (3, 1, 8192), (4, 2, 2048), (5, 1, 2048),
+                                    (6, 0, 2048)])
 def test_prefill_c3_shape(K, cb, M):
     """the 5120 -> 17408 prefill decode-GEMM (68 column tiles, split-K tail items) at the benchmark's K,
     codebook and row counts."""

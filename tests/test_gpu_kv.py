@@ -101,6 +101,24 @@ def test_kv_decode_32k():
     assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
 
 
+def test_kv_decode_c5_32k_4bit_batch16():
+    """The measured configuration at 32k context and 4-bit codes: B = 16, 40 / 8 heads, random page order."""
+    rng = np.random.default_rng(324)
+    lens = [32768] * 15 + [32768 - 9]
+    P = 16 * 2048
+    # random packed codes and scales straight away (quantizing 5e8 normal values on the host would take minutes)
+    kc, vc = (rng.integers(0, 256, size=(P, 8, PAGE, D // 2), dtype=np.uint8) for _ in range(2))
+    ks, vs = ((rng.random((P, 8)) * 0.02 + 0.01).astype(np.float16) for _ in range(2))
+    table = _table(rng, lens, 2048, P)
+    q = rng.standard_normal((16, 40, D)).astype(np.float16)
+    sm = D ** -0.5
+    y = _run(q, kc, vc, ks, vs, table, lens, 4, sm).cpu().numpy()
+    ref = orc.kv_decode_attention(q, kc, vc, ks, vs, table, np.asarray(lens, np.int32), 4, sm)
+    nrel, mrel = _errs(y, ref)
+    print(f"C5 32k 4-bit B=16: norm-rel {nrel:.2e} max-rel {mrel:.2e}")
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 def test_kv_decode_uniform_keys_give_mean_of_values(bits):
     """All-zero K codes: every logit is 0, so each head's output is the plain mean of its V rows (closed form)."""
