@@ -11,7 +11,7 @@ import re
 import threading
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libexl3_mi355x.so")
+LIB_PATH = os.environ.get("EXL3_MI355X_LIB") or os.path.join(PKG, "libexl3_mi355x.so")   # env: another build
 HEADER = os.path.join(os.path.dirname(PKG), "include", "exl3_mi355x.h")
 
 EXL3_OK, EXL3_ERR_INVALID, EXL3_ERR_HIP, EXL3_ERR_UNSUPPORTED = 0, 1, 2, 3

@@ -33,6 +33,26 @@ struct ShardArgs {
   int count;
 };
 
+// The fields of the shard that a wave-uniform 128-column block belongs to, chosen by compares over the (at most
+// EXL3_MAX_SHARDS) shards so that they stay in scalar registers.  Indexing the kernarg arrays with a computed shard
+// index made the compiler load the fields through vector registers and wrap every buffer load built on the trellis
+// base in a readfirstlane loop (five VALU and three SALU instructions a load, in every wave).
+struct ShardView {
+  const uint32_t* trellis;
+  const uint16_t* suh;
+  const uint16_t* svh;
+  int tn, col0, blk0;
+};
+
+__device__ __forceinline__ ShardView shard_of_block(const ShardArgs& sa, int blk) {
+  ShardView v{sa.trellis[0], sa.suh[0], sa.svh[0], sa.tn[0], sa.col0[0], sa.blk0[0]};
+#pragma unroll
+  for (int i = 1; i < EXL3_MAX_SHARDS; i++)
+    if (i < sa.count && blk >= sa.blk0[i])
+      v = ShardView{sa.trellis[i], sa.suh[i], sa.svh[i], sa.tn[i], sa.col0[i], sa.blk0[i]};
+  return v;
+}
+
 __device__ __forceinline__ int find_shard(const ShardArgs& sa, int blk) {
   int s = 0;
 #pragma unroll
@@ -215,7 +235,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
   const int blk = blockIdx.x, split = blockIdx.y;
-  const int s = find_shard(sa, blk);
+  const ShardView sh = shard_of_block(sa, blk);
   const int kb0 = split * NB;
   const int nb = min(k >> 7, kb0 + NB) - kb0;  // blocks of this split holding data (1..NB)
   constexpr int mstride = gemv_mstride(NT, DUP);
@@ -229,7 +249,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
-  const int tn = sa.tn[s];
+  const int tn = sh.tn;
   // prologue: activations of the split, rotated (or as given), into LDS; blocks past the split's end are zero.  One
   // (row, block) unit per half-wave.  When every half-wave has at most one unit, its activation loads are issued
   // before the trellis loads: loads complete in issue order, so the rotation then waits only for its own data and
@@ -242,20 +262,20 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
     if (single && hw < M * NB && b < nb) {
       const int kk = (kb0 + b) * 128 + 4 * t;
       xv = *reinterpret_cast<const uint2_t*>(static_cast<const uint16_t*>(x) + (size_t)m * k + kk);
-      if constexpr (ROTATE) sv = *reinterpret_cast<const uint2_t*>(sa.suh[s] + kk);
+      if constexpr (ROTATE) sv = *reinterpret_cast<const uint2_t*>(sh.suh + kk);
     }
   }
   __asm__ volatile("" ::: "memory");  // keep the activation loads ahead of the trellis loads
 
   Stream stream;
-  stream.init(sa.trellis[s], (k >> 4) * tn * 32 * K, tn, (blk - sa.blk0[s]) * kGemvWaves + w, kb0, nb,
+  stream.init(sh.trellis, (k >> 4) * tn * 32 * K, tn, (blk - sh.blk0) * kGemvWaves + w, kb0, nb,
               lds + gemv_a_bytes(M, NT, DUP) + w * Stream::LDS_BYTES, l);
   stream.start();
 
   if constexpr (PRE) {
     // prepared rows: 8-byte copies, all loads of the half-wave issued before the stores
     constexpr int IT = kGemvRows * NB / (2 * kGemvWaves);
-    const uint16_t* pre = static_cast<const uint16_t*>(x) + (size_t)s * pre_rows * k;
+    const uint16_t* pre = static_cast<const uint16_t*>(x) + (size_t)find_shard(sa, blk) * pre_rows * k;
     uint2_t v[IT];
 #pragma unroll
     for (int it = 0; it < IT; it++) {
@@ -306,9 +326,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       if (b < nb) {
         if constexpr (ROTATE) {
           if (x_bf16)
-            had_in_4<true>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
+            had_in_4<true>(static_cast<const uint16_t*>(x) + (size_t)m * k, sh.suh, kk, h);
           else
-            had_in_4<false>(static_cast<const uint16_t*>(x) + (size_t)m * k, sa.suh[s], kk, h);
+            had_in_4<false>(static_cast<const uint16_t*>(x) + (size_t)m * k, sh.suh, kk, h);
         } else {
           const half4_t v = *reinterpret_cast<const half4_t*>(static_cast<const uint16_t*>(x) + (size_t)m * k + kk);
           h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
@@ -383,7 +403,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
     const int m = tid >> 5, q = tid & 31;
     _Float16 h[4] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
     const int col = col_blk + 4 * q;
-    if constexpr (ROTATE) had_out_4(h, sa.svh[s] + (col - sa.col0[s]));
+    if constexpr (ROTATE) had_out_4(h, sh.svh + (col - sh.col0));
     uint16_t* yrow = static_cast<uint16_t*>(y) + (size_t)m * n_total;
     if (y_bf16)
       store_4<true>(yrow, col, h);
