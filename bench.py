@@ -9,7 +9,7 @@ One step = the four fused linears (decode-GEMV + rotations) over one batch of M 
 before timing starts; R rotating copies of the layer set (>= 512 MB, twice the 256 MB MALL) keep the weights cold.
 
 Prints one JSON line: metric/value = algorithmic HBM GB/s of the layer set at M = 1 (trellis + sign vectors +
-activations in/out, BASELINE.md C2 = 128,174,080 B per step), plus the roofline of the dominant kernel (the fused
+activations in/out: 128,174,080 B per step), plus the roofline of the dominant kernel (the fused
 decode-GEMV), the CPU baseline (the oracle's decode + matmul on up to 16 host cores, on a bounded sample), the
 M = 4 / 16 rates, and the other configs as reported fields: the single 4096 x 4096 linear of configs[0] (K = 4,
 3INST, M = 1), the prefill decode-GEMM TFLOPS (configs[2], `decode_gemm_tflops_m2048` is the second half of the
@@ -47,7 +47,7 @@ TRELLIS_BYTES_PER_STEP = sum(k * sum(ns) * K_BITS // 8 for k, ns in LAYERS.value
 
 
 def alg_bytes(k: int, ns: list[int], M: int, K: int) -> int:
-    """Trellis + suh per shard + svh + x in + y out (fp16), BASELINE.md C2."""
+    """Trellis + suh per shard + svh + x in + y out (fp16): the algorithmic bytes of one fused linear."""
     n = sum(ns)
     return k * n * K // 8 + 2 * k * len(ns) + 2 * n + 2 * M * k + 2 * M * n
 
@@ -152,7 +152,7 @@ KV_SHAPE = (16, 40, 8, 128)         # B, Hq, Hkv, head_dim
 
 
 def cpu_table(runs: int = 3, sample_tiles: int = 8192) -> dict:
-    """The CPU baseline of BASELINE.md section 3: the reference's CPU path (trellis_core reference.py:80-153) restated
+    """The CPU baseline: the reference's CPU path (trellis_core reference.py:80-153) restated
     in torch (oracle/torch_cpu.py) on the host's cores, median of `runs` runs, decode and matmul timed apart:
       C1  4096 x 4096, K = 4, 3INST, M = 1: the whole path (all 65536 tiles decoded);
       C2  the 27B layer set at M = 1 (K = 3, MCG), per layer, each source matrix as the reference runs it;

@@ -1,7 +1,7 @@
 // EXL3 prefill: fused decode-GEMM on gfx950 MFMA (v_mfma_f32_16x16x32_f16), y = Had(xh @ W_inner) * svh.
 //
 // Reference semantics: the reference's prefill is decode-to-HBM + cuBLAS between its rotation launches
-// (cuda/src/sglang_exl3/runtime/ops.py:36-59, SURVEY 3.2); the fused Marlin path serves < 256 rows
+// (cuda/src/sglang_exl3/runtime/ops.py:36-59); the fused Marlin path serves < 256 rows
 // (exl3_marlin_template.h).  Here the weights are decoded into LDS inside the GEMM and never reach HBM.
 //
 // Operands
@@ -18,13 +18,15 @@
 // lane).  135 KB of LDS: one workgroup per CU, CUs tiles at once.
 //
 // Work decomposition (1-D grid of work items, dispatched in order): tiles are numbered column block fastest, so
-// consecutive workgroups share their A rows in L2.  R x slots tiles (R whole rounds of the machine) are data-parallel
-// items covering all of k; the remaining tail tiles, too few to fill a round, are split along k into S items each
-// (S x tail <= slots) so that no round runs a few tiles on an otherwise idle chip.  The split items are dispatched
-// first: they fill the first round together with the first data-parallel tiles, and their reductions overlap the
-// rest of the launch.  A split item stores its fp32 accumulators as a partial; the last of the S items of a tile to
-// arrive (a per-tile counter in the workspace's counter region) sums the S partials in split order (deterministic,
-// independent of arrival order), then runs the same epilogue as a data-parallel item and resets the counter.
+// consecutive workgroups share their A rows in L2.  When the tile count is not a multiple of the machine's
+// workgroup slots, the last partial round and one full round before it (stream-K tiles) are shared out as equal runs
+// of k-steps over one workgroup per slot: a run crosses tile boundaries, so every workgroup finishes after the same
+// number of k-steps.  The stream-K workgroups are dispatched first, then one workgroup per remaining whole tile.  A
+// run's first and last segments can cover part of a tile: such a segment stores its fp32 accumulators as a partial,
+// and the last of the tile's workgroups to arrive (a per-tile counter in the workspace's counter region) sums the
+// tile's partials in workgroup order (deterministic, independent of arrival order), then runs the same epilogue as a
+// whole tile and resets the counter.  When whole rounds would finish sooner (the partials cost about a quarter of a
+// tile-time), every tile is a whole-tile item.
 //
 // Pipeline: direct-to-LDS 16-byte buffer loads (no VGPR staging) into two 3-slot rings, one for A (per k-step each
 // wave loads 2 pieces, one m-block of 64 lanes x 16 B each: a lane's 16 bytes land exactly where its MFMA A fragment
@@ -54,6 +56,8 @@ constexpr int kBStage = kBN * kBK * 2;            // 16 KB: [16 n-blocks][64 lan
 constexpr int kBitsStage = kGemmWaves * 64 * 16;  // 8 KB: per wave 64 lanes x 16 B (its 4 tiles of a k-step)
 constexpr int kRing = 3;                          // A and bits ring slots
 constexpr int kCStride = kBN + 8;                 // epilogue fp16 C tile row stride (halves)
+constexpr int kCoherentStore = 1 << 4;            // buffer cache policy sc1: device-scope coherent access
+constexpr int kPartialBytes = kBM * kBN * 4;      // one fp32 partial tile
 constexpr int kLoadRegion = kRing * (kAStage + kBitsStage) + 2 * kBStage;
 constexpr int kGemmLds = kLoadRegion > kBM * kCStride * 2 ? kLoadRegion : kBM * kCStride * 2;  // 135 KB: 1 per CU
 
@@ -70,13 +74,22 @@ struct GemmShards {
 // The work decomposition of one launch (see the header comment).
 struct GemmPlan {
   int nct;         // 256-column tiles per row block
-  int dp;          // data-parallel tiles 0 .. dp-1 (items tail * splits ..)
-  int tail;        // tail tiles dp .. dp+tail-1, split along k (items 0 .. tail * splits - 1)
-  int splits;      // k-splits of each tail tile
+  int sk_tiles;    // tiles 0 .. sk_tiles-1 are shared out by runs of k-steps among the stream-K workgroups
+  int groups;      // stream-K workgroups: grid items 0 .. groups-1; items groups.. are whole tiles sk_tiles..
   int ksteps;      // k / 32
-  float* partial;  // [tail items][8 waves][8][4][64 lanes] float4: a split item's accumulators
-  int* counters;   // [tail tiles], zero between calls
+  float* partial;  // [groups][2 segments][8 waves][8][4][64 lanes] float4: a workgroup's first / last segment
+  int* counters;   // [sk_tiles], zero between calls
 };
+
+// Stream-K: workgroup g owns the global k-steps [sk_start(g), sk_start(g + 1)) of the sk_tiles * ksteps steps (tile t
+// holds steps t * ksteps ..); sk_owner(q) is the workgroup whose run holds step q.
+__host__ __device__ __forceinline__ int64_t sk_start(const GemmPlan& p, int g) {
+  return (int64_t)p.sk_tiles * p.ksteps * g / p.groups;
+}
+__host__ __device__ __forceinline__ int sk_owner(const GemmPlan& p, int64_t q) {
+  const int64_t W = (int64_t)p.sk_tiles * p.ksteps;
+  return (int)(((q + 1) * p.groups + W - 1) / W) - 1;
+}
 
 // lds_barrier() (exl3_device.hpp) between k-steps: the direct-to-LDS writes are waited for explicitly (waitcnt_vm)
 // before each barrier.
@@ -127,31 +140,19 @@ __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict
   }
 }
 
+// One segment of work: k-steps [kt0, kt1) of tile `tile`.  seg < 0: the whole tile, straight to the epilogue;
+// seg = 0 / 1: a stream-K segment at the start / end of workgroup `item`'s run, stored as that partial slot; the
+// last of the tile's workgroups to arrive sums every partial of the tile in workgroup order and runs the epilogue.
 template <int K, int CB, bool Y_BF16>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmPlan plan, int M, int k,
-                                                             void* __restrict__ y, int n_total, int rotate_out) {
+__device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPlan& plan, int M, int k,
+                                             void* __restrict__ y, int n_total, int rotate_out, uint8_t* lds,
+                                             int item, int tile, int kt0, int kt1, int seg) {
   constexpr int CHUNKS = gemm_chunks<K>();
   static_assert(CHUNKS <= 64, "one gather per wave per k-step");
-  extern __shared__ __align__(16) uint8_t lds[];
   uint8_t* a_ring = lds;                             // [kRing][kAStage]
   uint8_t* bits_ring = lds + kRing * kAStage;        // [kRing][8 waves][64 lanes][16 B]
   uint8_t* b_lds = bits_ring + kRing * kBitsStage;   // [2][kBStage] decoded B fragments
 
-  // work item -> tile and k-step range: the split items of the tail tiles come first (dispatched while the machine
-  // fills, their reductions overlap the data-parallel tiles), then the data-parallel tiles
-  const int item = blockIdx.x;
-  const int nsplit = plan.tail * plan.splits;
-  int tile, kt0 = 0, kt1 = plan.ksteps, split = -1, sj = 0;
-  if (item >= nsplit) {
-    tile = item - nsplit;
-  } else {
-    sj = item;
-    const int tt = sj / plan.splits;
-    split = sj - tt * plan.splits;
-    tile = plan.dp + tt;
-    kt0 = (int)((int64_t)plan.ksteps * split / plan.splits);
-    kt1 = (int)((int64_t)plan.ksteps * (split + 1) / plan.splits);
-  }
   const int ct = tile % plan.nct, mblk = tile / plan.nct;
   int s = 0;
 #pragma unroll
@@ -288,51 +289,52 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // drain the trailing re-reads of every wave before LDS is reused
   __syncthreads();
 
-  // ---- split item: store the partial; the last of the tile's splits to arrive sums them all in split order
-  if (split >= 0) {
+  // ---- stream-K segment: store the partial (16-byte stores with device-scope coherence: the reader may sit on
+  // another XCD, whose L2 is not this one's); the tile's last workgroup to arrive sums all of the tile's partials in
+  // workgroup order (deterministic, independent of arrival order)
+  if (seg >= 0) {
     __shared__ int last_flag;
-    const int j0 = sj - split;  // the tile's first split item
-    float4_t* mine = reinterpret_cast<float4_t*>(plan.partial) + ((size_t)sj * kGemmWaves + w) * 32 * 64 + l;
+    const __amdgpu_buffer_rsrc_t prsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)plan.partial, (short)0, plan.groups * 2 * kGemmWaves * 32 * 64 * 16, 0x00020000);
+    auto slot_off = [&](int g, int sl) { return (((g * 2 + sl) * kGemmWaves + w) * 32 * 64 + l) * 16; };
+    const int mine = slot_off(item, seg);
 #pragma unroll
     for (int mi = 0; mi < 8; mi++)
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++) {
-        // device-scope coherent 8-byte stores: the partial is read by a workgroup that may sit on another XCD
-        const float4_t v = acc[mi][jj];
-        uint64_t* d = reinterpret_cast<uint64_t*>(mine + (mi * 4 + jj) * 64);
-        __hip_atomic_store(d, __builtin_bit_cast(uint64_t, f32x2{v.x, v.y}), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(d + 1, __builtin_bit_cast(uint64_t, f32x2{v.z, v.w}), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int jj = 0; jj < 4; jj++)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mi][jj]), prsrc,
+                                               mine + (mi * 4 + jj) * 64 * 16, 0, kCoherentStore);
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this thread's partial stores are at the coherence point
     __syncthreads();
-    const int tt = sj / plan.splits;
+    const int64_t q0 = (int64_t)tile * plan.ksteps;
+    const int g_first = sk_owner(plan, q0), g_last = sk_owner(plan, q0 + plan.ksteps - 1);
     if (tid == 0) {
-      const int prev = __hip_atomic_fetch_add(&plan.counters[tt], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_flag = prev == plan.splits - 1;
+      const int prev = __hip_atomic_fetch_add(&plan.counters[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = prev == g_last - g_first;
     }
     __syncthreads();
     if (!last_flag) return;
-#pragma unroll
-    for (int mi = 0; mi < 8; mi++)
-#pragma unroll
-      for (int jj = 0; jj < 4; jj++) acc[mi][jj] = float4_t{0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < plan.splits; sp++) {
-      const float4_t* src =
-          reinterpret_cast<const float4_t*>(plan.partial) + ((size_t)(j0 + sp) * kGemmWaves + w) * 32 * 64 + l;
+    // the sum runs in workgroup order from g_first; when this workgroup is g_first (the usual last arrival: the
+    // tile is the end of its run) its registers are that first term, bit for bit what it stored
+    int g = g_first;
+    if (item == g_first) {
+      g++;
+    } else {
 #pragma unroll
       for (int mi = 0; mi < 8; mi++)
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-          const uint64_t* d = reinterpret_cast<const uint64_t*>(src + (mi * 4 + jj) * 64);
-          const f32x2 a = __builtin_bit_cast(f32x2, __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-          const f32x2 b =
-              __builtin_bit_cast(f32x2, __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-          acc[mi][jj] += float4_t{a.x, a.y, b.x, b.y};
-        }
+        for (int jj = 0; jj < 4; jj++) acc[mi][jj] = float4_t{0.f, 0.f, 0.f, 0.f};
     }
-    if (tid == 0) __hip_atomic_store(&plan.counters[tt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (; g <= g_last; g++) {
+      const int src = slot_off(g, sk_start(plan, g) >= q0 ? 0 : 1);  // the tile is g's first segment or its last
+#pragma unroll
+      for (int mi = 0; mi < 8; mi++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+          acc[mi][jj] += __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          prsrc, src + (mi * 4 + jj) * 64 * 16, 0, kCoherentStore));
+    }
+    if (tid == 0) __hip_atomic_store(&plan.counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- epilogue: the whole fp16 C tile (256 x 256, rounded once from fp32) goes to LDS, then each thread rotates
@@ -401,6 +403,31 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
       }
     }
   }
+  __syncthreads();  // the C tile in LDS is read before the next segment's loads overwrite it
+}
+
+// Grid: the stream-K workgroups first (each walks the segments of its run of k-steps), then one workgroup per
+// remaining whole tile.
+template <int K, int CB, bool Y_BF16>
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmPlan plan, int M, int k,
+                                                             void* __restrict__ y, int n_total, int rotate_out) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int item = blockIdx.x;
+  if (item >= plan.groups) {
+    gemm_segment<K, CB, Y_BF16>(sa, plan, M, k, y, n_total, rotate_out, lds, item,
+                                plan.sk_tiles + (item - plan.groups), 0, plan.ksteps, -1);
+    return;
+  }
+  const int64_t a = sk_start(plan, item), b = sk_start(plan, item + 1);
+  for (int64_t q = a; q < b;) {
+    const int t = (int)(q / plan.ksteps);
+    const int64_t q0 = (int64_t)t * plan.ksteps;
+    const int kt0 = (int)(q - q0), kt1 = (int)(b - q0 < plan.ksteps ? b - q0 : plan.ksteps);
+    const bool whole = kt0 == 0 && kt1 == plan.ksteps;
+    gemm_segment<K, CB, Y_BF16>(sa, plan, M, k, y, n_total, rotate_out, lds, item, t, kt0, kt1,
+                                whole ? -1 : (q == a ? 0 : 1));
+    q = q0 + kt1;
+  }
 }
 
 #define EXL3_GEMM_DISPATCH(K_, CB_, ...)                                  \
@@ -433,7 +460,7 @@ static int gemm_slots() {
 }
 
 struct GemmLayout {
-  int nct, dp, splits, tail, ksteps;
+  int nct, sk_tiles, groups, ksteps, tiles;
   size_t xh_bytes, partial_off, total;
 };
 
@@ -445,26 +472,32 @@ static int gemm_col_tiles(const int* shard_n, int nshards) {  // tiles of 256 co
   return t;
 }
 
-// R whole rounds of data-parallel tiles, then the tail tiles split along k so that their items fill at most one
-// round; a split keeps >= 8 k-steps so its pipeline start-up stays small against its work
+// Whole tiles in rounds of the machine, except the last (partial) round plus one full round before it (when there
+// is one), which are shared out by runs of k-steps over one workgroup per slot (stream-K): every workgroup then
+// finishes after the same number of k-steps, 1 to 2 tiles' worth, and writes at most two partial tiles.  A run keeps
+// >= 8 k-steps so the pipeline start-up stays small against its work.  Whole rounds only, when they are sooner.
 static GemmLayout gemm_layout(int rows, int k, int nct, int nshards) {
   GemmLayout L{};
   L.nct = nct;
   L.ksteps = k / kBK;
-  const int tiles = ((rows + kBM - 1) / kBM) * nct;
+  L.tiles = ((rows + kBM - 1) / kBM) * nct;
   const int slots = gemm_slots();
-  L.dp = (tiles / slots) * slots;
-  L.tail = tiles - L.dp;
-  L.splits = 1;
-  if (L.tail > 0) L.splits = std::max(1, std::min(slots / L.tail, L.ksteps / 8));
-  if (L.splits == 1) {  // no split: the tail tiles are data-parallel items too
-    L.dp = tiles;
-    L.tail = 0;
+  const int rounds = L.tiles / slots, rem = L.tiles - rounds * slots;
+  if (rem > 0) {
+    const int sk = rounds >= 1 ? rem + slots : rem;
+    // in tile-times: whole tiles only take rounds + 1; stream-K takes the whole rounds left plus sk / slots plus the
+    // partial tiles' store, reload and wait (measured ~0.25 of a tile-time at 5120 -> 17408: 512 rows 156 us against
+    // 183 us whole, 768 rows 211 against 199)
+    const double whole = rounds + 1, shared = (double)(L.tiles - sk) / slots + (double)sk / slots + 0.25;
+    if (shared < whole) {
+      L.sk_tiles = sk;
+      L.groups = (int)std::max<int64_t>(1, std::min<int64_t>(slots, (int64_t)sk * L.ksteps / 8));
+    }
   }
-  // [counter region (fixed place and size)][rotated activations][partials]
+  // [counter region (fixed place and size)][rotated activations][partials: 2 per stream-K workgroup]
   L.xh_bytes = ((size_t)nshards * rows * k * 2 + 255) & ~(size_t)255;
   L.partial_off = kCounterBytes + L.xh_bytes;
-  L.total = L.partial_off + (size_t)L.tail * L.splits * kBM * kBN * sizeof(float);
+  L.total = L.partial_off + (size_t)L.groups * 2 * kPartialBytes;
   return L;
 }
 
@@ -516,9 +549,10 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   const GemmLayout L = gemm_layout(rows, k, gemm_col_tiles(shard_n, nshards), nshards);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= L.total, "exl3_linear_prefill: workspace %zu bytes, need %zu",
                  workspace_bytes, L.total);
-  EXL3_CHECK_ARG(L.tail <= kMaxCounters, "exl3_linear_prefill: %d tail tiles exceed the counter region", L.tail);
+  EXL3_CHECK_ARG(L.sk_tiles <= kMaxCounters, "exl3_linear_prefill: %d stream-K tiles exceed the counter region",
+                 L.sk_tiles);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  GemmPlan plan{L.nct, L.dp, L.tail, L.splits, L.ksteps, reinterpret_cast<float*>(ws + L.partial_off),
+  GemmPlan plan{L.nct, L.sk_tiles, L.groups, L.ksteps, reinterpret_cast<float*>(ws + L.partial_off),
                 reinterpret_cast<int*>(ws)};
   uint16_t* xh = reinterpret_cast<uint16_t*>(ws + kCounterBytes);
   hipStream_t st = as_stream(stream);
@@ -533,7 +567,7 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
           x, rows, k, static_cast<const uint16_t*>(shards_host[s].suh), 1, xh + (size_t)s * rows * k);
     EXL3_CHECK_LAUNCH();
   }
-  const dim3 grid((unsigned)(L.dp + L.tail * L.splits));
+  const dim3 grid((unsigned)(L.groups + L.tiles - L.sk_tiles));
   bool ok;
 #define EXL3_GEMM_LAUNCH(YB)                                                                                   \
   ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB><<<grid, kGemmThreads, kGemmLds, st>>>(      \
