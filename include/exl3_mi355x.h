@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 2
+#define EXL3_ABI_VERSION 3
 
 enum {
   EXL3_OK = 0,
@@ -153,6 +153,51 @@ int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const vo
                      int top_k, int num_experts, int inter, const exl3_moe_weights* weights_host, int K_gate_up,
                      int K_down, int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes,
                      void* stream);
+
+/* ---- MoE per-launch stages (the reference's moe_align_decode, moe_had_in, moe_gemm, moe_glu_had_in, moe_combine:
+ * cuda/csrc/exl3_marlin_moe.cu:376-618; run order cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294).  The same
+ * arithmetic as exl3_moe_forward, one launch per stage, for callers that drive the stages themselves.  Weights are the
+ * stored trellis stacks ([E][k/16][n/16][16K] per projection), not a repacked stack. */
+
+/* Routing in the layout of vLLM's moe_align_block_size for one block size (1..64): the slots of every expert (ids
+ * outside [0, num_experts), or mapped to -1 by expert_map, dropped) in ascending expert order, each expert's run
+ * padded to a multiple of `block` with the sentinel `slots`; expert_ids[i] = the expert of block i (expert_map[e]
+ * when a map is given, else e), -1 past the end; *num_post_padded = the padded length.  Slots keep no particular
+ * order inside a run.  sorted_ids holds cap >= slots + num_experts * (block - 1) entries (the sentinel past the
+ * end), expert_ids max_blocks >= cap / block.  One workgroup; num_experts <= 1024. */
+int exl3_moe_align(const int* topk_ids, int slots, int num_experts, const int* expert_map, int block, int* sorted_ids,
+                   int cap, int* expert_ids, int max_blocks, int* num_post_padded, void* stream);
+
+/* xh[s * slots + slot][k] = fp16(Had(fp16(x[slot / top_k]) * suh_s[e])) (x fp16 or bf16 [tokens][k]) for every slot
+ * with a valid expert e = topk_ids[slot] and every shard s < shards (1 or 2; suh: shards pointers to [E][k] fp16);
+ * rows of other slots are not written. */
+int exl3_moe_had_in(const void* x, int x_bf16, int tokens, int k, const int* topk_ids, int top_k, int num_experts,
+                    const void* const* suh, int shards, void* xh, void* stream);
+
+/* Workspace bytes of exl3_moe_gemm: the counter region (EXL3_WORKSPACE_COUNTER_BYTES, zero before the first use;
+ * every call leaves it zero) and fp32 split partials.  0 for bad shapes. */
+size_t exl3_moe_gemm_workspace_bytes(int rows, int k, int n, int shards, int max_blocks);
+
+/* The grouped expert GEMM: for every block i < *num_post_padded / block with expert e = expert_ids[i] in
+ * [0, num_experts) and every row r = sorted_ids[i * block + j] < rows,
+ *   c[r][s * n + col] = fp16(sum_k a[s * rows + r][k] * W_s[e][k][col])          (svh == NULL)
+ *   c[r][s * n + ...] = fp16(Had(fp16(acc)) * svh_s[e]) per 128 columns          (svh given: the output transform)
+ * for each shard s < shards (1 or 2: gate | up side by side).  a: fp16 [shards * rows][k]; trellis / svh: shards
+ * pointers to [E][k/16][n/16][16K] int16 / [E][n] fp16; c: fp16 [rows][shards * n]; other rows of c untouched. */
+int exl3_moe_gemm(const void* a, int rows, int k, const void* const* trellis, const void* const* svh, int shards, int n,
+                  const int* sorted_ids, const int* expert_ids, const int* num_post_padded, int max_blocks, int block,
+                  int num_experts, int K, int codebook, void* c, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* For every slot with a valid expert e = topk_ids[slot]: act[slot] = fp16(silu(g) * u) (fp32 SiLU; act may be
+ * NULL) and xd[slot] = fp16(Had(fp16(act * suh_down[e]))), from gu fp16 [slots][2 inter] = gate | up. */
+int exl3_moe_glu_had_in(const void* gu, int slots, int inter, const int* topk_ids, int num_experts,
+                        const void* suh_down, void* act, void* xd, void* stream);
+
+/* y[t] = sum over j of topk_weights[t][j] * yd[t * top_k + j] in fp32, slot order, one rounding (fp16 or bf16 y);
+ * slots whose id is outside [0, num_experts) are skipped. */
+int exl3_moe_combine(const void* yd, const float* topk_weights, const int* topk_ids, int tokens, int top_k, int hidden,
+                     int num_experts, void* y, int y_bf16, void* stream);
 
 /* ---- Quantized-KV paged decode attention (subsystem 5b) ------------------------------------------------------------ */
 /* The reference has no quantized-KV decode kernel: its nearest relative is the paged fp8 gather + dequant + blockwise

@@ -22,7 +22,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.exl3_abi_version() == 2
+    assert lib.exl3_abi_version() == 3
 
 
 def test_workspace_size_is_deterministic_and_zero_for_bad_shapes(lib):

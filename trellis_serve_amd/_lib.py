@@ -58,6 +58,13 @@ _SIGNATURES: dict[str, tuple] = {
     "exl3_moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I]),
     "exl3_moe_forward": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, ctypes.POINTER(Exl3MoeWeights), _I, _I, _I, _P,
                               _I, _P, _SZ, _P]),
+    "exl3_moe_align": (_I, [_P, _I, _I, _P, _I, _P, _I, _P, _I, _P, _P]),
+    "exl3_moe_had_in": (_I, [_P, _I, _I, _I, _P, _I, _I, ctypes.POINTER(_P), _I, _P, _P]),
+    "exl3_moe_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "exl3_moe_gemm": (_I, [_P, _I, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _I, _P, _P, _P, _I, _I, _I, _I, _I,
+                           _P, _P, _SZ, _P]),
+    "exl3_moe_glu_had_in": (_I, [_P, _I, _I, _P, _I, _P, _P, _P, _P]),
+    "exl3_moe_combine": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
     "exl3_kv_decode_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "exl3_kv_decode_attention": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I, _I, _I, _I, _I, _I, ctypes.c_float, _P,
                                       _P, _SZ, _P]),

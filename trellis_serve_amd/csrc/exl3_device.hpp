@@ -40,6 +40,9 @@ __device__ __forceinline__ _Float16 f16_of_f32(float p) {
 }
 __device__ __forceinline__ _Float16 had_scale_f16(float f) { return f16_of_f32(f * kHadScale); }
 
+// SiLU in fp32 (the MoE GLU, cuda/csrc/exl3_marlin_moe.cu:228-258)
+__device__ __forceinline__ float silu32(float v) { return v / (1.0f + __expf(-v)); }
+
 // s_waitcnt immediate for "vmcnt <= n" with expcnt and lgkmcnt unconstrained (gfx9 encoding: vmcnt bits 3:0 and
 // 15:14, expcnt 6:4, lgkmcnt 11:8)
 __host__ __device__ constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }

@@ -75,7 +75,6 @@ __host__ __device__ constexpr int moe_lds_bytes() {
 static_assert(moe_lds_bytes<8, 4, 16, true>() <= 160 * 1024, "MoE LDS must fit a CU");
 constexpr int kMoeMaxTopK = 64;
 
-__device__ __forceinline__ float silu32(float v) { return v / (1.0f + __expf(-v)); }
 
 // The rotated fp16 gate/up inputs fp16(Had(x[token] * suh)) at positions kk .. kk+3 (kk = 128 b + 4 t, lane t of a
 // half-wave); one 128-block per half-wave (had128_x4 spans 32 lanes).
@@ -526,7 +525,11 @@ static MoePhase moe_phase_plan(int slots, int rows, int nblk, int k, int K, int 
   const int C = (k / 128 + NB - 1) / NB;
   const double per_split = (double)slots * 8.0 / ((double)rows * k * std::max(K, 1) / 8.0);
   const int cap = std::max(1, (int)(0.25 / per_split));
-  const int want = std::max(1, (2048 + rows * nblk - 1) / (rows * nblk));
+  static const int target = [] {  // EXL3_MOE_TARGET_WGS: another workgroup target (A/B measurements)
+    const char* e = getenv("EXL3_MOE_TARGET_WGS");
+    return e ? std::max(1, atoi(e)) : 2048;
+  }();
+  const int want = std::max(1, (target + rows * nblk - 1) / (rows * nblk));
   const int s = std::min(C, std::min(cap, want));
   MoePhase ph{};
   ph.chunks = (C + s - 1) / s;
@@ -712,6 +715,26 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
     moe_combine_kernel<false><<<cgrid, 256, 0, st>>>(dn, static_cast<const int*>(topk_ids),
                                                      static_cast<const float*>(topk_weights), tokens, top_k,
                                                      num_experts, hidden, y);
+  EXL3_CHECK_LAUNCH();
+  return EXL3_OK;
+}
+
+extern "C" int exl3_moe_combine(const void* yd, const float* topk_weights, const int* topk_ids, int tokens, int top_k,
+                                int hidden, int num_experts, void* y, int y_bf16, void* stream) {
+  EXL3_CHECK_ARG(yd && topk_weights && topk_ids && y, "exl3_moe_combine: null pointer");
+  EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && hidden > 0 && hidden % 128 == 0 && num_experts >= 1,
+                 "exl3_moe_combine: tokens = %d, top_k = %d, hidden = %d, num_experts = %d", tokens, top_k, hidden,
+                 num_experts);
+  EXL3_CHECK_ARG((int64_t)tokens * top_k * hidden <= INT32_MAX, "exl3_moe_combine: too many rows");
+  if (tokens == 0) return EXL3_OK;
+  const dim3 grid((unsigned)(((size_t)tokens * (hidden / 128) + 7) / 8));
+  hipStream_t st = as_stream(stream);
+  if (y_bf16)
+    moe_combine_kernel<true><<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(yd), topk_ids, topk_weights, tokens,
+                                                   top_k, num_experts, hidden, y);
+  else
+    moe_combine_kernel<false><<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(yd), topk_ids, topk_weights, tokens,
+                                                    top_k, num_experts, hidden, y);
   EXL3_CHECK_LAUNCH();
   return EXL3_OK;
 }

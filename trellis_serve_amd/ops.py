@@ -93,7 +93,7 @@ class _Workspace:
         self.reserved = True
 
 
-_KINDS = {"linear": True, "prefill": True, "moe": True, "kv": False}
+_KINDS = {"linear": True, "prefill": True, "moe": True, "moe_stage": True, "kv": False}
 _workspaces: dict[tuple[str, int], _Workspace] = {}
 
 
@@ -359,6 +359,160 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Ten
                                     out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(), ws.numel(),
                                     _stream(x.device)),
                "moe_forward")
+    return out
+
+
+# ---- MoE per-launch stages: the launches the reference's unfused path runs after moe_align_block_size
+# (cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294: moe_had_in, moe_gemm for gate|up, moe_glu_had_in, moe_gemm for
+# down, moe_combine), on the stored trellis stacks
+
+def _routing_ids(topk_ids: torch.Tensor, device: torch.device) -> torch.Tensor:
+    if topk_ids.dtype not in (torch.int32, torch.int64) or topk_ids.device != device:
+        raise ValueError(f"topk_ids must be int32/int64 on {device}, got {topk_ids.dtype} on {topk_ids.device}")
+    return topk_ids.to(torch.int32).contiguous()
+
+
+def _ptr_array(tensors: list[torch.Tensor]):
+    return (ctypes.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
+
+
+def moe_align(topk_ids: torch.Tensor, num_experts: int, block: int, expert_map: torch.Tensor | None = None):
+    """(sorted_ids, expert_ids, num_post_padded) in the layout of vLLM's moe_align_block_size for one block size
+    (the reference's moe_align_decode, cuda/csrc/exl3_marlin_moe.cu:546-618): each expert's slots padded to a multiple
+    of `block` with the sentinel topk_ids.numel(), the expert (or expert_map[e]) of every block, -1 past the end."""
+    ids = _routing_ids(topk_ids, topk_ids.device).reshape(-1)
+    slots = ids.numel()
+    cap = slots + num_experts * (block - 1)
+    max_blocks = -(-cap // block)
+    dev = ids.device
+    sorted_ids = torch.empty(cap, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(max_blocks, dtype=torch.int32, device=dev)
+    post = torch.empty(1, dtype=torch.int32, device=dev)
+    emap = None
+    if expert_map is not None:
+        if expert_map.numel() != num_experts:
+            raise ValueError(f"expert_map holds {expert_map.numel()} entries for {num_experts} experts")
+        emap = _routing_ids(expert_map, dev)
+    _lib.check(_lib.load().exl3_moe_align(ids.data_ptr(), slots, int(num_experts), _ptr(emap), int(block),
+                                          sorted_ids.data_ptr(), cap, expert_ids.data_ptr(), max_blocks,
+                                          post.data_ptr(), _stream(dev)), "moe_align")
+    return sorted_ids, expert_ids, post
+
+
+def moe_had_in(x: torch.Tensor, suh: list[torch.Tensor], topk_ids: torch.Tensor,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """xh [shards * slots, k] fp16: fp16(Had(fp16(x[token]) * suh_s[e])) per (shard, slot) (the reference's
+    moe_had_in, cuda/csrc/exl3_marlin_moe.cu:416-448); suh: one [E, k] fp16 stack per shard (gate, up)."""
+    if x.dtype not in (torch.float16, torch.bfloat16) or x.dim() != 2:
+        raise ValueError("x must be a 2-D fp16/bf16 tensor")
+    T, k = x.shape
+    ids = _routing_ids(topk_ids, x.device)
+    if ids.dim() != 2 or ids.shape[0] != T:
+        raise ValueError(f"topk_ids {tuple(topk_ids.shape)} must be [{T}, top_k]")
+    if not 1 <= len(suh) <= 2:
+        raise ValueError("one or two suh stacks")
+    E = suh[0].shape[0]
+    for t in suh:
+        if t.dtype != torch.float16 or tuple(t.shape) != (E, k) or not t.is_contiguous() or t.device != x.device:
+            raise ValueError(f"suh stacks must be contiguous fp16 [{E}, {k}] on {x.device}")
+    slots = ids.numel()
+    if out is None:
+        out = torch.empty((len(suh) * slots, k), dtype=torch.float16, device=x.device)
+    _check_out(out, (len(suh) * slots, k), x, (torch.float16,))
+    _lib.check(_lib.load().exl3_moe_had_in(x.contiguous().data_ptr(), int(x.dtype == torch.bfloat16), T, k,
+                                           ids.data_ptr(), ids.shape[1], E, _ptr_array(suh), len(suh),
+                                           out.data_ptr(), _stream(x.device)), "moe_had_in")
+    return out
+
+
+def moe_gemm(a: torch.Tensor, trellis: list[torch.Tensor], svh: list[torch.Tensor] | None, sorted_ids: torch.Tensor,
+             expert_ids: torch.Tensor, num_post_padded: torch.Tensor, block: int, codebook: int,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """The grouped expert GEMM over align blocks (the reference's moe_gemm, cuda/csrc/exl3_marlin_moe.cu:376-412):
+    a fp16 [shards * rows, k] (rotated inputs), trellis one [E, k/16, n/16, 16K] stack per shard; returns c fp16
+    [rows, shards * n], with the output transform fp16(Had(fp16(acc)) * svh) when svh stacks ([E, n]) are given."""
+    if a.dtype != torch.float16 or a.dim() != 2 or not a.is_contiguous():
+        raise ValueError("a must be a contiguous fp16 [shards * rows, k] tensor")
+    shards = len(trellis)
+    if shards not in (1, 2) or a.shape[0] % shards:
+        raise ValueError(f"one or two trellis stacks; a has {a.shape[0]} rows")
+    rows, k = a.shape[0] // shards, a.shape[1]
+    t0 = trellis[0]
+    if any(t.dtype != torch.int16 or t.dim() != 4 or t.shape != t0.shape or not t.is_contiguous()
+           or t.device != a.device for t in trellis):
+        raise ValueError("trellis stacks must be contiguous int16 [E, k/16, n/16, 16K] of one shape on a's device")
+    E, n, K = t0.shape[0], t0.shape[2] * 16, bits_of(t0)
+    if t0.shape[1] * 16 != k:
+        raise ValueError(f"trellis input width {t0.shape[1] * 16} != {k}")
+    if svh is not None:
+        if len(svh) != shards or any(v.dtype != torch.float16 or tuple(v.shape) != (E, n) or not v.is_contiguous()
+                                     or v.device != a.device for v in svh):
+            raise ValueError(f"svh must be {shards} contiguous fp16 [{E}, {n}] stacks")
+    for name, t in (("sorted_ids", sorted_ids), ("expert_ids", expert_ids), ("num_post_padded", num_post_padded)):
+        if t.dtype != torch.int32 or not t.is_contiguous() or t.device != a.device:
+            raise ValueError(f"{name} must be a contiguous int32 tensor on {a.device}")
+    max_blocks = expert_ids.numel()
+    if max_blocks * block < sorted_ids.numel():
+        raise ValueError(f"expert_ids ({max_blocks}) too short for {sorted_ids.numel()} sorted ids in blocks of {block}")
+    if out is None:
+        out = torch.empty((rows, shards * n), dtype=torch.float16, device=a.device)
+    _check_out(out, (rows, shards * n), a, (torch.float16,))
+    if rows == 0:
+        return out
+    lib = _lib.load()
+    ws = workspace(a.device, lib.exl3_moe_gemm_workspace_bytes(rows, k, n, shards, max_blocks), "moe_stage")
+    _lib.check(lib.exl3_moe_gemm(a.data_ptr(), rows, k, _ptr_array(trellis), None if svh is None else _ptr_array(svh),
+                                 shards, n, sorted_ids.data_ptr(), expert_ids.data_ptr(), num_post_padded.data_ptr(),
+                                 max_blocks, int(block), E, K, int(codebook), out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                 _stream(a.device)), "moe_gemm")
+    return out
+
+
+def moe_glu_had_in(gu: torch.Tensor, suh_down: torch.Tensor, topk_ids: torch.Tensor, act: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(act, xd): act = fp16(silu(g) * u) and the rotated down inputs xd = fp16(Had(fp16(act * suh_down[e]))) per slot
+    from gu fp16 [slots, 2 inter] (the reference's moe_glu_had_in, cuda/csrc/exl3_marlin_moe.cu:450-477)."""
+    if gu.dtype != torch.float16 or gu.dim() != 2 or not gu.is_contiguous() or gu.shape[1] % 256:
+        raise ValueError("gu must be a contiguous fp16 [slots, 2 inter] tensor")
+    slots, inter = gu.shape[0], gu.shape[1] // 2
+    ids = _routing_ids(topk_ids, gu.device).reshape(-1)
+    if ids.numel() != slots:
+        raise ValueError(f"topk_ids holds {ids.numel()} slots, gu {slots}")
+    if suh_down.dtype != torch.float16 or suh_down.dim() != 2 or suh_down.shape[1] != inter \
+            or not suh_down.is_contiguous() or suh_down.device != gu.device:
+        raise ValueError(f"suh_down must be a contiguous fp16 [E, {inter}] stack")
+    if act is None:
+        act = torch.empty((slots, inter), dtype=torch.float16, device=gu.device)
+    if out is None:
+        out = torch.empty((slots, inter), dtype=torch.float16, device=gu.device)
+    _check_out(act, (slots, inter), gu, (torch.float16,))
+    _check_out(out, (slots, inter), gu, (torch.float16,))
+    _lib.check(_lib.load().exl3_moe_glu_had_in(gu.data_ptr(), slots, inter, ids.data_ptr(), suh_down.shape[0],
+                                               suh_down.data_ptr(), act.data_ptr(), out.data_ptr(),
+                                               _stream(gu.device)), "moe_glu_had_in")
+    return act, out
+
+
+def moe_combine(yd: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor, num_experts: int,
+                out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """y [tokens, hidden] = sum_j w[t, j] * yd[t * top_k + j] in fp32, slot order, one rounding; slots with ids outside
+    [0, num_experts) skipped (the reference's moe_combine, cuda/csrc/exl3_marlin_moe.cu:479-500)."""
+    if yd.dtype != torch.float16 or yd.dim() != 2 or not yd.is_contiguous():
+        raise ValueError("yd must be a contiguous fp16 [slots, hidden] tensor")
+    ids = _routing_ids(topk_ids, yd.device)
+    if ids.dim() != 2 or tuple(topk_weights.shape) != tuple(ids.shape) or ids.numel() != yd.shape[0]:
+        raise ValueError(f"topk_ids {tuple(ids.shape)} / topk_weights {tuple(topk_weights.shape)} do not match "
+                         f"{yd.shape[0]} rows")
+    if topk_weights.device != yd.device:
+        raise ValueError("topk_weights must be on yd's device")
+    w = topk_weights.to(torch.float32).contiguous()
+    T, top_k = ids.shape
+    if out is None:
+        out = torch.empty((T, yd.shape[1]), dtype=out_dtype, device=yd.device)
+    _check_out(out, (T, yd.shape[1]), yd)
+    _lib.check(_lib.load().exl3_moe_combine(yd.data_ptr(), w.data_ptr(), ids.data_ptr(), T, top_k, yd.shape[1],
+                                            int(num_experts), out.data_ptr(), int(out.dtype == torch.bfloat16),
+                                            _stream(yd.device)), "moe_combine")
     return out
 
 
