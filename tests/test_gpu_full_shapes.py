@@ -69,3 +69,36 @@ def test_prefill_c3_shape(K, cb, M):
     trs, suhs, svhs = _layer(g, 5120, [17408], K)
     x = (torch.randn((M, 5120), generator=g) * 0.5).half().cuda()
     _check(_ops().linear_prefill(x, trs, suhs, svhs, cb), _reference(x, trs, suhs, svhs, cb))
+
+
+@pytest.mark.parametrize("name,M,K,cb,fn", [("gate_up", 1, 3, 1, "linear"), ("down", 4, 3, 1, "linear"),
+                                            ("c3", 2048, 3, 1, "linear_prefill"), ("c3", 8192, 5, 2, "linear_prefill")])
+def test_full_shape_column_slices_against_the_oracle(coracle, name, M, K, cb, fn):
+    """The full-shape outputs, checked on sampled 128-column blocks and rows against the float64 oracle built from the
+    C restatement's decode (the output rotation works per 128-column block, so a block of columns is a complete
+    smaller layer): full-size parity that does not rest on this library's own reconstruct and rotation kernels."""
+    import numpy as np
+    from conftest import c_reconstruct
+    from oracle import exl3_oracle as orc
+    k, ns = (5120, [17408]) if name == "c3" else C2_LAYERS[name]
+    g = torch.Generator(device="cpu").manual_seed(300 + M + K)
+    trs, suhs, svhs = _layer(g, k, ns, K)
+    x = (torch.randn((M, k), generator=g) * 0.5).half().cuda()
+    y = getattr(_ops(), fn)(x, trs, suhs, svhs, cb).float().cpu().numpy()
+    rng = np.random.default_rng(M)
+    rows = np.sort(rng.choice(M, size=min(M, 48), replace=False))
+    xs = x.cpu().numpy()[rows]
+    col = 0
+    for tr, suh, svh in zip(trs, suhs, svhs):
+        tn = tr.shape[1]
+        trn = tr.cpu().numpy()
+        for cbk in rng.choice(tn // 8, size=min(3, tn // 8), replace=False):
+            sl = trn[:, 8 * cbk:8 * cbk + 8]
+            w = c_reconstruct(coracle, sl, K, cb)
+            sv = svh.cpu().numpy()[128 * cbk:128 * cbk + 128]
+            ref = orc.linear_forward(xs, sl, suh.cpu().numpy(), sv, K, cb, w_inner=w, dtype=np.float64)
+            got = y[rows][:, col + 128 * cbk:col + 128 * cbk + 128].astype(np.float64)
+            nrel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+            mrel = np.abs(got - ref).max() / np.abs(ref).max()
+            assert nrel <= TOL and mrel <= TOL, (cbk, nrel, mrel)
+        col += tn * 16
