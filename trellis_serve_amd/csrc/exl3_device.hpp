@@ -187,23 +187,54 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 // ---- 128-point Hadamard on 32 lanes x 4 values (lane t holds block positions 4t..4t+3) -----------------------
 // Sylvester order: H128 = H32 (lanes) x H4 (in-lane); the in-lane part is the 4-point butterfly, the lane part five
 // xor-butterflies.  fp32 throughout, as cuda/csrc/exl3_had.cuh:20-84.
+//
+// The partner value of a lane-xor stage comes from the VALU's cross-lane paths, not the LDS unit (ds_bpermute):
+// xor 1 and 2 are DPP quad permutes, xor 8 a DPP row rotate by 8, xor 4 two DPP row rotates (by 12 and by 4: the
+// lanes whose bit 2 is clear take the lane 4 above, the others the lane 4 below; neither wraps inside the 16-lane
+// row; row_ror:n gives lane i the value of lane i - n of its row), xor 16 v_permlane16_swap (rows 2r and 2r+1).  Each stage computes partner + (+-own): the lower lane
+// a + b and the upper lane a - b of the pair (a, b), exactly the sums of the xor-shuffle form.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  if constexpr (M == 1) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+  } else if constexpr (M == 2) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+  } else if constexpr (M == 4) {
+    const int up = __builtin_amdgcn_mov_dpp(x, 0x12C, 0xF, 0xF, false);  // row_ror:12 -> lane i + 4 of the row
+    const int dn = __builtin_amdgcn_mov_dpp(x, 0x124, 0xF, 0xF, false);  // row_ror:4  -> lane i - 4 of the row
+    return __builtin_bit_cast(float, (__lane_id() & 4) ? dn : up);
+  } else if constexpr (M == 8) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false));  // row_ror:8
+  } else {
+    static_assert(M == 16, "lane xor 1, 2, 4, 8 or 16");
+    // with both operands x the swap returns (x of the even row, x of the odd row) in every lane of the row pair
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return __builtin_bit_cast(float, (int)((__lane_id() & 16) ? p[0] : p[1]));
+  }
+}
+
+template <int M>
+__device__ __forceinline__ void had_stage(float& h0, float& h1, float& h2, float& h3) {
+  const uint32_t flip = (__lane_id() & M) ? 0x80000000u : 0u;  // the upper lane subtracts its own value
+  auto step = [&](float& h) { h = lane_xor<M>(h) + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, h) ^ flip); };
+  step(h0);
+  step(h1);
+  step(h2);
+  step(h3);
+}
+
 __device__ __forceinline__ void had128_x4(float& h0, float& h1, float& h2, float& h3) {
   const float s0 = h0 + h1, d0 = h0 - h1, s1 = h2 + h3, d1 = h2 - h3;
   h0 = s0 + s1;
   h1 = d0 + d1;
   h2 = s0 - s1;
   h3 = d0 - d1;
-  const int lane = __lane_id();
-#pragma unroll
-  for (int m = 1; m < 32; m <<= 1) {
-    const bool upper = lane & m;
-    const float o0 = __shfl_xor(h0, m, 64), o1 = __shfl_xor(h1, m, 64);
-    const float o2 = __shfl_xor(h2, m, 64), o3 = __shfl_xor(h3, m, 64);
-    h0 = upper ? o0 - h0 : h0 + o0;
-    h1 = upper ? o1 - h1 : h1 + o1;
-    h2 = upper ? o2 - h2 : h2 + o2;
-    h3 = upper ? o3 - h3 : h3 + o3;
-  }
+  had_stage<1>(h0, h1, h2, h3);
+  had_stage<2>(h0, h1, h2, h3);
+  had_stage<4>(h0, h1, h2, h3);
+  had_stage<8>(h0, h1, h2, h3);
+  had_stage<16>(h0, h1, h2, h3);
 }
 
 }  // namespace exl3
