@@ -212,7 +212,8 @@ size_t exl3_kv_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_hea
  * page_table[b][0 .. ceil(seq_lens[b] / 16)); query head h reads KV head h / (Hq / Hkv) (Hq / Hkv <= 16).
  * q fp16 [B][Hq][128], page_table int32 [B][max_pages], seq_lens int32 [B], out fp16 [B][Hq][128].  A sequence of
  * length 0 gives zeros; page ids outside [0, num_pages) are clamped (never read outside the cache).  head_dim must be
- * 128 and page_size 16.  Two launches (split-KV over page chunks, then the log-sum-exp merge); deterministic. */
+ * 128 and page_size 16.  Two launches (split-KV over page chunks, then the log-sum-exp merge), one when a single chunk
+ * covers every sequence; deterministic. */
 int exl3_kv_decode_attention(const void* q, const void* k_cache, const void* v_cache, const void* k_scale,
                              const void* v_scale, int num_pages, const void* page_table, int max_pages,
                              const void* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,

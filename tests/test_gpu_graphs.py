@@ -123,10 +123,11 @@ def test_moe_graph_after_reservation():
     assert _ws_ptr("moe") == ptr
 
 
-def test_kv_graph_after_reservation():
+@pytest.mark.parametrize("max_pages", [64, 4])   # 16 chunks and a merge launch / one chunk, no merge launch
+def test_kv_graph_after_reservation(max_pages):
     ops = _ops()
-    g = torch.Generator().manual_seed(61)
-    B, Hq, Hkv, D, max_pages = 4, 16, 4, 128, 64
+    g = torch.Generator().manual_seed(61 + max_pages)
+    B, Hq, Hkv, D = 4, 16, 4, 128
     P = B * max_pages
     kc = torch.randint(-128, 128, (P, Hkv, 16, D), dtype=torch.int8, generator=g).cuda()
     vc = torch.randint(-128, 128, (P, Hkv, 16, D), dtype=torch.int8, generator=g).cuda()

@@ -64,7 +64,7 @@ def _case(seed, lens, Hq, Hkv, bits, max_pages=None, extra_pages=3):
 
 @pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("lens,Hq,Hkv", [([1, 17, 300], 40, 8), ([16, 33, 1000, 64], 8, 8), ([255, 4], 32, 2),
-                                         ([2049], 40, 8)])
+                                         ([2049], 40, 8), ([1, 40, 64], 40, 8)])   # the last: one chunk, no merge
 def test_kv_decode_matches_closed_form(bits, lens, Hq, Hkv):
     q, kc, vc, ks, vs, table = _case(7 + len(lens) + bits, lens, Hq, Hkv, bits)
     sm = D ** -0.5

@@ -209,7 +209,8 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
     const _Float16* __restrict__ q, const uint8_t* kc, const uint8_t* vc, const _Float16* ksc, const _Float16* vsc,
     int num_pages,
     const int* __restrict__ page_table, int max_pages, const int* __restrict__ seq_lens, int Hq, int Hkv,
-    float qk_scale, int chunk_pages, float* __restrict__ part_o, float* __restrict__ part_ml) {
+    float qk_scale, int chunk_pages, float* __restrict__ part_o, float* __restrict__ part_ml,
+    _Float16* __restrict__ out) {
   constexpr int ROW = KvRegs<BITS>::ROW;
   extern __shared__ float red[];  // [4 waves][G][D + 1] then [4 waves][G][2]
   const int chunk = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
@@ -302,6 +303,13 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
     const float* src = red_o + (ww * G + tq) * (kHeadDim + 1) + td;
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[e] += src[e] * f;
+  }
+  if (gridDim.x == 1) {  // one chunk per sequence: its state is the result (no merge launch)
+    half8_t h;
+#pragma unroll
+    for (int e = 0; e < 8; e++) h[e] = (_Float16)(lsum > 0.f ? acc[e] / lsum : 0.f);
+    *reinterpret_cast<half8_t*>(out + ((size_t)b * Hq + hk * G + tq) * kHeadDim + td) = h;
+    return;
   }
   const size_t slot = (((size_t)b * Hkv + hk) * gridDim.x + chunk) * G + tq;
   float4_t* po = reinterpret_cast<float4_t*>(part_o + slot * kHeadDim + td);
@@ -428,10 +436,12 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
                                     kv_decode_kernel<8, 5>}};
   table[bits == 8][depth - 2]<<<grid, kKvWaves * 64, lds, st>>>(qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl,
                                                                 num_q_heads, num_kv_heads, qk_scale, cp, part_o,
-                                                                part_ml);
+                                                                part_ml, static_cast<_Float16*>(out));
   EXL3_CHECK_LAUNCH();
-  kv_merge_kernel<<<dim3(num_q_heads, batch), 256, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
-                                                             static_cast<_Float16*>(out));
-  EXL3_CHECK_LAUNCH();
+  if (chunks > 1) {
+    kv_merge_kernel<<<dim3(num_q_heads, batch), 256, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
+                                                               static_cast<_Float16*>(out));
+    EXL3_CHECK_LAUNCH();
+  }
   return EXL3_OK;
 }
