@@ -154,7 +154,8 @@ def test_chained_stages_match_exact_layer_and_fused_forward(T, cb, K_down, block
     assert np.abs(y - fused).max() <= 2e-3 * np.abs(fused).max()
     # the GLU stage's own outputs: act = fp16(silu(g) * u) from the fp16 g|u rows
     valid = (ids.reshape(-1) >= 0) & (ids.reshape(-1) < E)   # unrouted slots hold no defined g|u rows
-    g, u = gu[valid, :I].float().cpu().numpy(), gu[valid, I:].float().cpu().numpy()
+    guf = gu.float().cpu().numpy()[valid]
+    g, u = guf[:, :I], guf[:, I:]
     want_act = (orc.silu32(g) * u).astype(np.float16)
     got_act = act.cpu().numpy()[valid].view(np.int16).astype(np.int32)
     assert np.abs(got_act - want_act.view(np.int16).astype(np.int32)).max() <= 1   # fp32 exp within an ulp
