@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 3
+#define EXL3_ABI_VERSION 4
 
 enum {
   EXL3_OK = 0,
@@ -62,6 +62,13 @@ int exl3_init_device(int device);
  * trellis_core.reference.reconstruct_inner (core/src/trellis_core/reference.py:102-115).  Replaces ExLlamaV3's
  * `reconstruct` as called at cuda/src/sglang_exl3/kernels/reference.py:71-76 and xpu/csrc/exl3_ops.sycl:536. */
 int exl3_reconstruct(const void* trellis, int k, int n, int K, int codebook, void* w_out, void* stream);
+/* Load-time repack of a stored trellis int16 [k/16][n/16][16K] into the layout the kernels read.  Replaces
+ * repack_trellis (cuda/csrc/exl3_marlin.cu:344-381, called by prepare, cuda/src/sglang_exl3/kernels/marlin.py:65-76).
+ * The gfx950 kernels read the stored layout itself, so the repacked form is the stored form: `out` receives a copy of
+ * the k*n*K/8 bytes (nothing happens when out == trellis).  Lossless; exl3_unpack_trellis inverts it. */
+int exl3_repack_trellis(const void* trellis, int k, int n, int K, void* out, void* stream);
+/* Inverse of exl3_repack_trellis: the stored layout back.  Replaces unpack_trellis (exl3_marlin.cu:384-408). */
+int exl3_unpack_trellis(const void* packed, int k, int n, int K, void* out, void* stream);
 
 /* ---- Hadamard rotations (subsystem 4) ------------------------------------------------------------------------- */
 /* xh[s*rows + r, :] = fp16(Had128(fp16(x[r, :]) * suh_cat[s, :])) for shards s < shards; xh fp16 [shards*rows, k].

@@ -22,7 +22,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.exl3_abi_version() == 3
+    assert lib.exl3_abi_version() == 4
 
 
 def test_workspace_size_is_deterministic_and_zero_for_bad_shapes(lib):
@@ -37,6 +37,9 @@ def test_workspace_size_is_deterministic_and_zero_for_bad_shapes(lib):
     (lambda l: l.exl3_reconstruct(None, 256, 256, 3, 1, None, None), "null"),
     (lambda l: l.exl3_reconstruct(1, 256, 256, 7, 1, 1, None), "K = 7"),
     (lambda l: l.exl3_reconstruct(1, 256, 256, 3, 5, 1, None), "codebook = 5"),
+    (lambda l: l.exl3_repack_trellis(None, 256, 256, 3, 1, None), "null"),
+    (lambda l: l.exl3_repack_trellis(1, 256, 256, 7, 2, None), "K = 7"),
+    (lambda l: l.exl3_unpack_trellis(1, 250, 256, 3, 2, None), "k = 250"),
     (lambda l: l.exl3_had_in_group(1, 0, 4, 100, 1, 1, 1, None), "k = 100"),
     (lambda l: l.exl3_had_in_group(1, 0, 4, 128, 1, 5, 1, None), "shards = 5"),
     (lambda l: l.exl3_had_out_into(1, 4, 128, 1, 1, 0, 64, 0, None), "ld_out"),

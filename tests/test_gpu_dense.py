@@ -94,6 +94,24 @@ def test_gemm_rotated_one_hot_readout_is_exact(coracle, K, cb):
     np.testing.assert_array_equal(w.view(np.uint16), c_reconstruct(coracle, tr, K, cb).view(np.uint16))
 
 
+@pytest.mark.parametrize("K", KS)
+def test_repack_is_lossless_and_the_kernels_read_it(coracle, K):
+    """repack -> unpack returns the stored trellis bit for bit (the invertibility check of
+    cuda/src/sglang_exl3/parity/marlin_parity.py:173), in place as well, and the repacked form decodes to the
+    oracle's weights."""
+    rng = np.random.default_rng(500 + K)
+    tr = _trellis(rng, 256, 384, K)
+    t = torch.from_numpy(tr).cuda()
+    ops = _ops()
+    packed = ops.repack_trellis(t)
+    assert packed.data_ptr() != t.data_ptr()
+    np.testing.assert_array_equal(ops.unpack_trellis(packed).cpu().numpy(), tr)
+    assert ops.repack_trellis(t, out=t).data_ptr() == t.data_ptr()
+    np.testing.assert_array_equal(t.cpu().numpy(), tr)
+    w = ops.reconstruct(packed, 1).cpu().numpy()
+    np.testing.assert_array_equal(w.view(np.uint16), c_reconstruct(coracle, tr, K, 1).view(np.uint16))
+
+
 @pytest.mark.parametrize("K", (2, 3, 4))
 @pytest.mark.parametrize("cb", CBS)
 def test_one_hot_readout_through_the_split_k_gemv_is_exact(coracle, K, cb):

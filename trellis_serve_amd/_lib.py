@@ -46,6 +46,8 @@ _SIGNATURES: dict[str, tuple] = {
     "exl3_last_error": (ctypes.c_char_p, []),
     "exl3_init_device": (_I, [_I]),
     "exl3_reconstruct": (_I, [_P, _I, _I, _I, _I, _P, _P]),
+    "exl3_repack_trellis": (_I, [_P, _I, _I, _I, _P, _P]),
+    "exl3_unpack_trellis": (_I, [_P, _I, _I, _I, _P, _P]),
     "exl3_had_in_group": (_I, [_P, _I, _I, _I, _P, _I, _P, _P]),
     "exl3_had_out_into": (_I, [_P, _I, _I, _P, _P, _I, _I, _I, _P]),
     "exl3_linear_workspace_bytes": (_SZ, [_I, _I, _I, _I]),

@@ -634,6 +634,28 @@ extern "C" int exl3_reconstruct(const void* trellis, int k, int n, int K, int co
   return EXL3_OK;
 }
 
+// The load-time layout of the kernels is the stored one (each lane reads its two trellis words straight from the tile
+// as stored; a tile-column-major layout measured no faster), so the repack and its inverse are the identity on the
+// bytes: a device copy, or nothing when the output is the input.
+static int trellis_identity(const char* what, const void* in, int k, int n, int K, void* out, void* stream) {
+  EXL3_CHECK_ARG(in && out, "%s: null pointer", what);
+  EXL3_CHECK_ARG(valid_bits(K), "%s: K = %d", what, K);
+  EXL3_CHECK_ARG(k > 0 && n > 0 && k % 16 == 0 && n % 16 == 0, "%s: k = %d, n = %d", what, k, n);
+  if (in == out) return EXL3_OK;
+  const size_t bytes = (size_t)k * n * K / 8;
+  const hipError_t e = hipMemcpyAsync(out, in, bytes, hipMemcpyDeviceToDevice, as_stream(stream));
+  if (e != hipSuccess) return set_error(EXL3_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return EXL3_OK;
+}
+
+extern "C" int exl3_repack_trellis(const void* trellis, int k, int n, int K, void* out, void* stream) {
+  return trellis_identity("exl3_repack_trellis", trellis, k, n, K, out, stream);
+}
+
+extern "C" int exl3_unpack_trellis(const void* packed, int k, int n, int K, void* out, void* stream) {
+  return trellis_identity("exl3_unpack_trellis", packed, k, n, K, out, stream);
+}
+
 extern "C" int exl3_had_in_group(const void* x, int x_bf16, int rows, int k, const void* suh_cat, int shards,
                                  void* xh, void* stream) {
   EXL3_CHECK_ARG(x && suh_cat && xh, "exl3_had_in_group: null pointer");

@@ -192,6 +192,27 @@ def reconstruct(trellis: torch.Tensor, codebook: int, out: torch.Tensor | None =
     return out
 
 
+def repack_trellis(trellis: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The trellis in the layout the kernels read (the reference's repack_trellis, cuda/csrc/exl3_marlin.cu:344-381):
+    the stored int16 [k/16, n/16, 16K] layout itself, so the result is a copy (or `out` = the input: nothing to do)."""
+    return _trellis_identity(trellis, out, "exl3_repack_trellis")
+
+
+def unpack_trellis(packed: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Inverse of repack_trellis (the reference's unpack_trellis, exl3_marlin.cu:384-408)."""
+    return _trellis_identity(packed, out, "exl3_unpack_trellis")
+
+
+def _trellis_identity(t: torch.Tensor, out: torch.Tensor | None, entry: str) -> torch.Tensor:
+    k, n, K = _check_trellis(t)
+    if out is None:
+        out = torch.empty_like(t)
+    if out.shape != t.shape or out.dtype != torch.int16 or not out.is_contiguous() or out.device != t.device:
+        raise ValueError(f"out must be a contiguous int16 {tuple(t.shape)} tensor on {t.device}")
+    _lib.check(getattr(_lib.load(), entry)(t.data_ptr(), k, n, K, out.data_ptr(), _stream(t.device)), entry)
+    return out
+
+
 def had_in_group(x: torch.Tensor, suh_cat: torch.Tensor, xh: torch.Tensor | None = None) -> torch.Tensor:
     """xh[s] = fp16(Had128(fp16(x) * suh_cat[s])) for all shards: x fp16|bf16 [rows, k] -> fp16 [shards*rows, k]
     (kernels/marlin.py:138-146)."""
