@@ -318,11 +318,15 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
         (void*)plan.partial, (short)0, plan.groups * 2 * kGemmWaves * 32 * 64 * 16, 0x00020000);
     auto slot_off = [&](int g, int sl) { return (((g * 2 + sl) * kGemmWaves + w) * 32 * 64 + l) * 16; };
     const int mine = slot_off(item, seg);
+    // only the 16-row blocks that hold output rows (rows >= M and columns past a half tile are never stored), so a
+    // few-row prefill moves a fraction of the 256 KB per partial
+    const int live_rows = mfma_wave ? M - row0 - wm * 128 : 0;  // wave-uniform
 #pragma unroll
     for (int mi = 0; mi < 8; mi++)
+      if (mi * 16 < live_rows)
 #pragma unroll
-      for (int jj = 0; jj < 4; jj++)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mi][jj]), prsrc,
+        for (int jj = 0; jj < 4; jj++)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mi][jj]), prsrc,
                                                mine + (mi * 4 + jj) * 64 * 16, 0, kCoherentStore);
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this thread's partial stores are at the coherence point
     __syncthreads();
@@ -349,9 +353,10 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
       const int src = slot_off(g, sk_start(plan, g) >= q0 ? 0 : 1);  // the tile is g's first segment or its last
 #pragma unroll
       for (int mi = 0; mi < 8; mi++)
+        if (mi * 16 < live_rows)
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
-          acc[mi][jj] += __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+          for (int jj = 0; jj < 4; jj++)
+            acc[mi][jj] += __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                           prsrc, src + (mi * 4 + jj) * 64 * 16, 0, kCoherentStore));
     }
     if (tid == 0) __hip_atomic_store(&plan.counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

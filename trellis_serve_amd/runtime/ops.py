@@ -5,7 +5,10 @@ row-count dispatch, dtype handling and output allocation live inside the op so a
 Dispatch (the reference's `_linear`, runtime/ops.py:62-126, with MI355X switch points):
   rows < PREFILL_ROWS  -> fused decode-GEMV (exl3_linear, up to 16 rows per launch)
   rows >= PREFILL_ROWS -> fused decode-GEMM (exl3_linear_prefill)
-PREFILL_ROWS comes from measured crossovers on the 27B shapes (GEMV faster up to ~80-200 rows).
+PREFILL_ROWS comes from measured crossovers on the 27B shapes: the GEMV streams the weights once per 16 rows, the
+fused GEMM once for up to 256 rows; at 33-48 rows (three GEMV passes) the two are within a few percent on every
+layer of the set, from 49 rows (four passes) the GEMM is faster on every layer (64 rows: gate/up 146 vs 106 us, down
+100 vs 78, q/k/v 62 vs 51, o 56 vs 53).
 """
 from __future__ import annotations
 
@@ -15,7 +18,7 @@ import torch
 
 from .. import ops as _kernels
 
-PREFILL_ROWS = int(os.environ.get("EXL3_MI355X_PREFILL_ROWS", "128"))
+PREFILL_ROWS = int(os.environ.get("EXL3_MI355X_PREFILL_ROWS", "48"))
 
 _lib = torch.library.Library("exl3_mi355x", "FRAGMENT")  # must stay alive at module scope
 
