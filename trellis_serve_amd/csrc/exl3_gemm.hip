@@ -163,7 +163,9 @@ __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict
 // One segment of work: k-steps [kt0, kt1) of tile `tile`.  seg < 0: the whole tile, straight to the epilogue;
 // seg = 0 / 1: a stream-K segment at the start / end of workgroup `item`'s run, stored as that partial slot; the
 // last of the tile's workgroups to arrive sums every partial of the tile in workgroup order and runs the epilogue.
-template <int K, int CB, bool Y_BF16>
+// FEW (a launch of fewer than 256 rows, one row block): the MFMAs and A-fragment reads of 16-row blocks past M are
+// skipped (their accumulators stay zero and are never stored); every load, decode and barrier is unchanged.
+template <int K, int CB, bool Y_BF16, bool FEW>
 __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPlan& plan, int M, int k,
                                              void* __restrict__ y, int n_total, int rotate_out, uint8_t* lds,
                                              int item, int tile, int kt0, int kt1, int seg) {
@@ -190,6 +192,8 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
   const int wm = w >> 2, wn = w & 3;  // wave tile: rows 128 wm .., columns 64 wn ..
   const int c = l & 15, j = l >> 4;
   const bool mfma_wave = 4 * wn < ntc;  // wave-uniform: its 64 columns exist
+  // 16-row blocks of the wave tile that hold rows below M (wave-uniform; all 8 unless FEW)
+  const int live_mi = FEW ? max(0, min(8, (M - row0 - wm * 128 + 15) / 16)) : 8;
 
   // B: wave w loads and decodes tile row btr = w >> 2, tile columns btc .. btc+3 (btc = 4 (w & 3)) of every k-step;
   // past the end of a half tile it re-reads the tile's first columns (in range, decoded into n-blocks nobody reads)
@@ -287,12 +291,14 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
 #pragma unroll
       for (int jj = 0; jj < 4; jj++) bv[jj] = bf[jj * 64];
 #pragma unroll
-      for (int mi = 0; mi < 8; mi++) av[mi] = af[mi * 64];
+      for (int mi = 0; mi < 8; mi++)
+        if (mi < live_mi) av[mi] = af[mi * 64];
 #pragma unroll
       for (int mi = 0; mi < 8; mi++)
+        if (mi < live_mi)
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
-          acc[mi][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mi], bv[jj], acc[mi][jj], 0, 0, 0);
+          for (int jj = 0; jj < 4; jj++)
+            acc[mi][jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mi], bv[jj], acc[mi][jj], 0, 0, 0);
     }
     // the next step's weights (at the last step: a stale but valid stage into a buffer nobody reads)
     write_b(i + 1, bw);
@@ -320,7 +326,7 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
     const int mine = slot_off(item, seg);
     // only the 16-row blocks that hold output rows (rows >= M and columns past a half tile are never stored), so a
     // few-row prefill moves a fraction of the 256 KB per partial
-    const int live_rows = mfma_wave ? M - row0 - wm * 128 : 0;  // wave-uniform
+    const int live_rows = mfma_wave ? M - row0 - wm * 128 : 0;  // wave-uniform (mi * 16 < live_rows: mi < live_mi)
 #pragma unroll
     for (int mi = 0; mi < 8; mi++)
       if (mi * 16 < live_rows)
@@ -433,13 +439,13 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
 
 // Grid: the stream-K workgroups first (each walks the segments of its run of k-steps), then one workgroup per
 // remaining whole tile.
-template <int K, int CB, bool Y_BF16>
+template <int K, int CB, bool Y_BF16, bool FEW>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmPlan plan, int M, int k,
                                                              void* __restrict__ y, int n_total, int rotate_out) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int item = blockIdx.x;
   if (item >= plan.groups) {
-    gemm_segment<K, CB, Y_BF16>(sa, plan, M, k, y, n_total, rotate_out, lds, item,
+    gemm_segment<K, CB, Y_BF16, FEW>(sa, plan, M, k, y, n_total, rotate_out, lds, item,
                                 plan.sk_tiles + (item - plan.groups), 0, plan.ksteps, -1);
     return;
   }
@@ -449,7 +455,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmShards sa, GemmP
     const int64_t q0 = (int64_t)t * plan.ksteps;
     const int kt0 = (int)(q - q0), kt1 = (int)(b - q0 < plan.ksteps ? b - q0 : plan.ksteps);
     const bool whole = kt0 == 0 && kt1 == plan.ksteps;
-    gemm_segment<K, CB, Y_BF16>(sa, plan, M, k, y, n_total, rotate_out, lds, item, t, kt0, kt1,
+    gemm_segment<K, CB, Y_BF16, FEW>(sa, plan, M, k, y, n_total, rotate_out, lds, item, t, kt0, kt1,
                                 whole ? -1 : (q == a ? 0 : 1));
     q = q0 + kt1;
   }
@@ -593,13 +599,18 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   EXL3_CHECK_LAUNCH();
   const dim3 grid((unsigned)(L.groups + L.tiles - L.sk_tiles));
   bool ok;
-#define EXL3_GEMM_LAUNCH(YB)                                                                                   \
-  ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB><<<grid, kGemmThreads, kGemmLds, st>>>(      \
+#define EXL3_GEMM_LAUNCH(YB, FEW)                                                                              \
+  ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB, FEW><<<grid, kGemmThreads, kGemmLds, st>>>( \
                                           sa, plan, rows, k, y, col, 1))
-  if (y_bf16)
-    EXL3_GEMM_LAUNCH(true);
+  const bool few = rows < kBM;  // one row block, mostly rows past M
+  if (y_bf16 && few)
+    EXL3_GEMM_LAUNCH(true, true);
+  else if (y_bf16)
+    EXL3_GEMM_LAUNCH(true, false);
+  else if (few)
+    EXL3_GEMM_LAUNCH(false, true);
   else
-    EXL3_GEMM_LAUNCH(false);
+    EXL3_GEMM_LAUNCH(false, false);
 #undef EXL3_GEMM_LAUNCH
   if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_linear_prefill: unsupported K/codebook");
   EXL3_CHECK_LAUNCH();

@@ -6,9 +6,9 @@ Dispatch (the reference's `_linear`, runtime/ops.py:62-126, with MI355X switch p
   rows < PREFILL_ROWS  -> fused decode-GEMV (exl3_linear, up to 16 rows per launch)
   rows >= PREFILL_ROWS -> fused decode-GEMM (exl3_linear_prefill)
 PREFILL_ROWS comes from measured crossovers on the 27B shapes: the GEMV streams the weights once per 16 rows, the
-fused GEMM once for up to 256 rows; at 33-48 rows (three GEMV passes) the two are within a few percent on every
-layer of the set, from 49 rows (four passes) the GEMM is faster on every layer (64 rows: gate/up 146 vs 106 us, down
-100 vs 78, q/k/v 62 vs 51, o 56 vs 53).
+fused GEMM once for up to 256 rows.  Up to 32 rows (two GEMV passes) the GEMV is faster on every layer of the set;
+from three passes the GEMM is faster on the layer set as a whole (40 rows: gate/up 114 vs 95 us, down 74 vs 69,
+q/k/v 46 vs 46, o 42 vs 48; 64 rows: 148 vs 96, 101 vs 74, 62 vs 49, 57 vs 52).
 """
 from __future__ import annotations
 
@@ -18,7 +18,7 @@ import torch
 
 from .. import ops as _kernels
 
-PREFILL_ROWS = int(os.environ.get("EXL3_MI355X_PREFILL_ROWS", "48"))
+PREFILL_ROWS = int(os.environ.get("EXL3_MI355X_PREFILL_ROWS", "33"))
 
 _lib = torch.library.Library("exl3_mi355x", "FRAGMENT")  # must stay alive at module scope
 
