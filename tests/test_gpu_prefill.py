@@ -108,3 +108,22 @@ def test_prefill_split_tail_tiles_match_oracle(coracle):
         assert nrel <= TOL and mrel <= TOL, (rows, cols, nrel, mrel)
     for _ in range(3):
         assert torch.equal(_ops().linear_prefill(_dev(x), *args), y)
+
+
+@pytest.mark.parametrize("M", [1, 16, 40, 255])
+@pytest.mark.parametrize("n", [512, 384])
+def test_prefill_few_rows_many_contributors(coracle, M, n):
+    """Under 256 rows with only 1-2 column tiles and a long k: every tile is shared out over many stream-K workgroups
+    (tens of fp32 partials per tile, each holding only the row blocks below M; the MFMAs of row blocks past M are
+    skipped).  Against the float64 oracle and repeatable bit for bit."""
+    rng = np.random.default_rng(300 + M + n)
+    k, K, cb = 6144, 3, 1
+    tr, suh, svh = _case(rng, k, n, K)
+    x = (rng.standard_normal((M, k)) * 0.5).astype(np.float16)
+    args = ([_dev(tr)], [_dev(suh)], [_dev(svh)], cb)
+    y = _ops().linear_prefill(_dev(x), *args)
+    ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
+    nrel, mrel = _errs(y.cpu().numpy(), ref)
+    assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
+    for _ in range(2):
+        assert torch.equal(_ops().linear_prefill(_dev(x), *args), y)
