@@ -150,9 +150,11 @@ def test_gemv_shards_of_uneven_widths(coracle, M, cb):
     assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 17])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 17, 24, 32, 45])
 @pytest.mark.parametrize("K,cb", [(2, 1), (3, 1), (4, 0), (5, 2), (6, 1), (8, 0)])
 def test_linear_matches_float64_oracle(coracle, M, K, cb):
+    """Up to 16 rows one MFMA row group per decoded tile, 17-32 two groups in one launch (rows padded with zeros to
+    32), past 32 rows another launch for the rest."""
     rng = np.random.default_rng(3000 + 100 * M + 10 * K + cb)
     k, n = 768, 640
     tr, suh, svh = _trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)
@@ -176,7 +178,7 @@ def test_linear_c1_shape_4096(coracle):
     assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
 
 
-@pytest.mark.parametrize("rows,k,n", [(4, 512, 384), (16, 4096, 16384)])
+@pytest.mark.parametrize("rows,k,n", [(4, 512, 384), (16, 4096, 16384), (29, 4096, 16384), (20, 512, 384)])
 def test_linear_bf16_boundary_equals_fp16_casts(rows, k, n):
     """run(x_bf16) == run(x_bf16.half()).bfloat16() bit for bit (cuda/src/sglang_exl3/parity/marlin_parity.py:98-111);
     16 rows of a 4096 -> 16384 linear take the path that rotates the input once per shard before the GEMV."""
@@ -288,3 +290,25 @@ def test_workspace_shared_by_calls_of_different_shapes(coracle):
         ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
         nrel, mrel = _errs(y, ref)
         assert nrel <= TOL and mrel <= TOL, (k, n, M, nrel, mrel)
+
+
+@pytest.mark.parametrize("rows", [17, 32])
+def test_two_row_groups_match_oracle_with_prepared_rows(coracle, rows):
+    """Two 16-row groups share each decoded tile: at 17 rows every workgroup rotates its rows, at 32 rows (64 column
+    blocks x 32 rows x 32 k-blocks) the input is rotated once per shard before the GEMV; both shards against the
+    float64 oracle, repeatable bit for bit."""
+    rng = np.random.default_rng(70 + rows)
+    k, K, cb = 4096, 3, 1
+    ns = (4096, 4096)
+    cases = [(_trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)) for n in ns]
+    args = ([_dev(c[0]) for c in cases], [_dev(c[1]) for c in cases], [_dev(c[2]) for c in cases], cb)
+    x = (rng.standard_normal((rows, k)) * 0.5).astype(np.float16)
+    y = _ops().linear(_dev(x), *args)
+    col = 0
+    for (tr, suh, svh), n in zip(cases, ns):
+        w = c_reconstruct(coracle, tr[:, :64], K, cb)   # the first 1024 columns of the shard
+        ref = orc.linear_forward(x, tr[:, :64], suh, svh[:1024], K, cb, w_inner=w, dtype=np.float64)
+        nrel, mrel = _errs(y[:, col:col + 1024].cpu().numpy(), ref)
+        assert nrel <= TOL and mrel <= TOL, (n, nrel, mrel)
+        col += n
+    assert torch.equal(_ops().linear(_dev(x), *args), y)

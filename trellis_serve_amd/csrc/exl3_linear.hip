@@ -20,7 +20,8 @@
 namespace exl3 {
 
 constexpr int kGemvWaves = 8;   // one wave per tile column: a workgroup covers one 128-column block
-constexpr int kGemvRows = 16;   // rows per launch (the M of MFMA 16x16x16)
+constexpr int kGemvRows = 16;   // rows of one MFMA row group (the M of MFMA 16x16x16)
+constexpr int kGemvPairRows = 32;  // rows per launch with two row groups per decoded tile (gemv_kernel<..., P = 2>)
 constexpr int kGemvMaxLds = 65536;  // dynamic LDS limit of a workgroup without opt-in
 
 struct ShardArgs {
@@ -223,14 +224,17 @@ __host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K, bool dup)
 
 // PRE: x is the rotated activations of every shard, [shards][pre_rows][k] in A-staging order (had_in_kernel<.., true>),
 // staged by plain 8-byte copies; else x is the input rows, rotated here (ROTATE) or taken as given
-template <int K, int CB, bool ROTATE, int NT, bool PRE = false>
+// P = 2 (17-32 rows): every decoded tile feeds two 16-row MFMA groups (rounded fp16 weights, v_mfma 16x16x16): the
+// weights stream once for 32 rows instead of once per 16.  The staged rows are padded with zeros to 32.
+template <int K, int CB, bool ROTATE, int NT, bool PRE = false, int P = 1>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
                                                              int M, int k, int splits, float* partial,
                                                              int* counters, void* __restrict__ y,
                                                              int y_bf16, int n_total, int pre_rows = 0) {
-  typedef TileStream<K, CB, NT, false, true> Stream;
+  typedef TileStream<K, CB, NT, false, P == 1> Stream;
   constexpr int NB = Stream::NB;
-  constexpr bool DUP = Stream::DUP;  // activations staged twice for the two-halves decode (MCG, 3INST)
+  constexpr bool DUP = Stream::DUP;  // activations staged twice for the two-halves decode (MCG, 3INST, one group)
+  const int Mp = P == 1 ? M : kGemvRows * ((M + kGemvRows - 1) / kGemvRows);  // staged rows; rows M .. Mp-1 are 0
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
@@ -255,7 +259,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   // before the trellis loads: loads complete in issue order, so the rotation then waits only for its own data and
   // runs while the trellis blocks are in flight.
   const int hw = threadIdx.x >> 5, t = threadIdx.x & 31;
-  const bool single = !PRE && M * NB <= 2 * kGemvWaves;
+  const bool single = !PRE && Mp * NB <= 2 * kGemvWaves;
   uint2_t xv = uint2_t{0u, 0u}, sv = uint2_t{0u, 0u};
   if constexpr (!PRE) {
     const int m = hw / NB, b = hw - m * NB;
@@ -269,7 +273,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
   Stream stream;
   stream.init(sh.trellis, (k >> 4) * tn * 32 * K, tn, (blk - sh.blk0) * kGemvWaves + w, kb0, nb,
-              lds + gemv_a_bytes(M, NT, DUP) + w * Stream::LDS_BYTES, l);
+              lds + gemv_a_bytes(Mp, NT, DUP) + w * Stream::LDS_BYTES, l);
   // Trellis blocks issued before the prologue.  Every workgroup's activation loads queue behind the trellis loads
   // the CU's workgroups issued before them, so the prologue (and with it the first MFMA) waits less with fewer early
   // blocks; the rest of the three in flight follow the prologue's barrier (layer set at one row: 79.2 -> 78.2 us).
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
   if constexpr (PRE) {
     // prepared rows: 8-byte copies, all loads of the half-wave issued before the stores
-    constexpr int IT = kGemvRows * NB / (2 * kGemvWaves);
+    constexpr int IT = kGemvRows * P * NB / (2 * kGemvWaves);
     const uint16_t* pre = static_cast<const uint16_t*>(x) + (size_t)find_shard(sa, blk) * pre_rows * k;
     uint2_t v[IT];
 #pragma unroll
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
     for (int it = 0; it < IT; it++) {
       const int u = hw + it * 2 * kGemvWaves;
       const int m = u / NB, b = u - m * NB;
-      if (u < M * NB) {
+      if (u < Mp * NB) {  // rows M .. Mp-1 store the zeros v was set to
         if constexpr (DUP) {  // the 4 staged halves, each twice
           uint32_t d[4] = {__builtin_amdgcn_perm(v[it].x, v[it].x, 0x01000100u),
                            __builtin_amdgcn_perm(v[it].x, v[it].x, 0x03020302u),
@@ -307,10 +311,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       }
     }
   } else if (single) {
-    if (hw < M * NB) {
+    if (hw < Mp * NB) {
       const int m = hw / NB, b = hw - m * NB;
       _Float16 h[4] = {0, 0, 0, 0};
-      if (b < nb) {
+      if (b < nb && m < M) {
         if constexpr (ROTATE) {
           if (x_bf16)
             had_in_raw<true>(xv, sv, h);
@@ -325,11 +329,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       for (int i = 0; i < 4; i++) stage1(b * 128 + 4 * t + i, m, h[i]);
     }
   } else {
-    for (int u = hw; u < M * NB; u += 2 * kGemvWaves) {
+    for (int u = hw; u < Mp * NB; u += 2 * kGemvWaves) {
       const int m = u / NB, b = u - m * NB;
       const int kk = (kb0 + b) * 128 + 4 * t;
       _Float16 h[4] = {0, 0, 0, 0};
-      if (b < nb) {
+      if (b < nb && m < M) {
         if constexpr (ROTATE) {
           if (x_bf16)
             had_in_4<true>(static_cast<const uint16_t*>(x) + (size_t)m * k, sh.suh, kk, h);
@@ -349,11 +353,17 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   for (int b = kEarly; b < 3 && b < NB; b++) stream.issue(b);
 
   // A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored
-  float4_t acc;
-  if constexpr (DUP)
-    acc = stream.run_dup(reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j);
-  else
-    acc = stream.run(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j);
+  float4_t acc[P];
+  if constexpr (P > 1) {
+#pragma unroll
+    for (int p = 0; p < P; p++) acc[p] = float4_t{0.f, 0.f, 0.f, 0.f};
+    stream.template run_groups<P>(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j,
+                                  kGemvRows * mstride / 4, Mp / kGemvRows, acc);
+  } else if constexpr (DUP) {
+    acc[0] = stream.run_dup(reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j);
+  } else {
+    acc[0] = stream.run(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j);
+  }
 
 
   // this split's partial; C layout: lane l holds rows 4(l/16) + r, column l % 16.  Partials cross XCDs (each XCD
@@ -364,10 +374,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       __builtin_amdgcn_make_buffer_rsrc((void*)partial, (short)0, splits * M * n_total * 4, 0x00020000);
   float* pdst = partial + (size_t)split * M * n_total + col_blk + w * 16 + c;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int m = 4 * j + r;
-    if (m < M) __hip_atomic_store(pdst + (size_t)m * n_total, acc[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  for (int p = 0; p < P; p++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int m = kGemvRows * p + 4 * j + r;
+      if (m < M)
+        __hip_atomic_store(pdst + (size_t)m * n_total, acc[p][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this thread's partial stores are at the coherence point
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -378,13 +391,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   if (!last_flag) return;
 
   // last split of this column block: units (row m, 4-column group q); p-groups G share the splits p = g, g + G, ...
-  // and are combined in a fixed order
+  // and are combined in a fixed order.  Past 16 rows the units take two passes of 512.
   float4_t* red = reinterpret_cast<float4_t*>(lds);  // reuse the LDS (>= 512 * 16 B reserved)
-  const int units = M * 32;
-  const int G = max(1, kGemvThreads / units);
   const int tid = threadIdx.x;
+  for (int u0 = 0; u0 < M * 32; u0 += kGemvThreads) {
+  const int units = min(M * 32 - u0, kGemvThreads);
+  const int G = max(1, kGemvThreads / units);
   if (tid < units * G) {
-    const int unit = tid % units, gq = tid / units;
+    const int unit = u0 + tid % units, gq = tid / units;
     const int m = unit >> 5, q = unit & 31;
     const int base = (m * n_total + col_blk + 4 * q) * 4;
     const int pstride = M * n_total * 4;
@@ -402,13 +416,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       for (int i = 0; i < 8; i++)
         if (p0 + i * G < splits) a += v[i];
     }
-    red[gq * units + unit] = a;
+    red[gq * units + unit - u0] = a;
   }
   __syncthreads();
   if (tid < units) {
     float4_t a = red[tid];
     for (int gq = 1; gq < G; gq++) a += red[gq * units + tid];
-    const int m = tid >> 5, q = tid & 31;
+    const int m = (u0 + tid) >> 5, q = tid & 31;
     _Float16 h[4] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
     const int col = col_blk + 4 * q;
     if constexpr (ROTATE) had_out_4(h, sh.svh + (col - sh.col0));
@@ -417,6 +431,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       store_4<true>(yrow, col, h);
     else
       store_4<false>(yrow, col, h);
+  }
+  __syncthreads();  // the next pass reuses red
   }
   if (tid == 0) __hip_atomic_store(&counters[blk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -442,20 +458,22 @@ static int gemv_target_wgs(int M) {
 }
 
 // pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there.
-// cb: MCG / 3INST stage the activations twice (more LDS per tile row)
+// cb: MCG / 3INST stage the activations twice (more LDS per tile row) when one row group serves the launch; past 16
+// rows (two groups, P = 2) the activations are staged once, padded to 32 rows
 static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = false) {
   const int kb = k / 128, nblk = n_total / 128;
-  const bool dup = cb != CB_MUL1;
+  const bool dup = cb != CB_MUL1 && M <= kGemvRows;
+  const int Ms = M <= kGemvRows ? M : kGemvPairRows;
   int nt = 16;
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
     if (pre && cand > 32) continue;
-    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs(M) && gemv_lds_bytes(M, cand, K, dup) <= kGemvMaxLds) {
+    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs(M) && gemv_lds_bytes(Ms, cand, K, dup) <= kGemvMaxLds) {
       nt = cand;
       break;
     }
   }
-  return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(M, nt, K, dup)};
+  return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(Ms, nt, K, dup)};
 }
 
 // workspace layout: [counter region: one int per 128-column block, zero between calls][fp32 partials]; the region
@@ -519,11 +537,12 @@ static bool gemv_pre(int rows, int k, int n_total) {
   return rows >= kGemvPreRows && (size_t)(n_total / 128) * rows * (k / 128) >= kGemvPreUnits;
 }
 
-// workspace layout: [counter region][fp32 partials of the largest 16-row launch][rotated rows, when gemv_pre]; the
-// size does not depend on the codebook (the largest plan of either staging form)
-static size_t gemv_partial_bytes(int rows, int k, int n_total, int K) {
+// workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre]; the size does
+// not depend on the codebook (the largest plan of either staging form).  launch_rows: rows per launch, 16, or 32 where
+// two row groups share each decoded tile (exl3_linear)
+static size_t gemv_partial_bytes(int rows, int k, int n_total, int K, int launch_rows) {
   size_t need = 0;
-  for (int M : {std::min(rows, kGemvRows), rows % kGemvRows}) {
+  for (int M : {std::min(rows, launch_rows), rows % launch_rows}) {
     if (M == 0) continue;
     for (int cb : {(int)CB_MCG, (int)CB_MUL1}) {
       const GemvPlan pl = gemv_plan(k, n_total, M, K, cb, gemv_pre(rows, k, n_total));
@@ -536,13 +555,19 @@ static size_t gemv_pre_bytes(int rows, int k, int n_total) {
   return gemv_pre(rows, k, n_total) ? (size_t)EXL3_MAX_SHARDS * rows * k * 2 : 0;
 }
 
+static size_t gemv_workspace_bytes(int rows, int k, int n_total, int K, int launch_rows) {
+  return counters_bytes(n_total) + gemv_partial_bytes(rows, k, n_total, K, launch_rows) +
+         gemv_pre_bytes(rows, k, n_total);
+}
+
+// launch_rows: 32 (two row groups per decoded tile past 16 rows; rotated launches only) or 16
 static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_bf16, int rows, int k, int K, int cb,
-                       int n_total, void* workspace, void* y, bool y_bf16, hipStream_t st) {
+                       int n_total, void* workspace, void* y, bool y_bf16, hipStream_t st, int launch_rows) {
   int* counters = static_cast<int*>(workspace);
   float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total));
   const bool pre = rotate && gemv_pre(rows, k, n_total);
   uint16_t* xh = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total) +
-                                             gemv_partial_bytes(rows, k, n_total, K));
+                                             gemv_partial_bytes(rows, k, n_total, K, launch_rows));
   if (pre) {
     const dim3 hgrid((unsigned)(((size_t)sa.count * rows * (k / 128) + 7) / 8));
     if (x_bf16)
@@ -551,15 +576,30 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
       had_in_shards_kernel<false><<<hgrid, 256, 0, st>>>(x, rows, k, sa, xh);
     EXL3_CHECK_LAUNCH();
   }
-  for (int r0 = 0; r0 < rows; r0 += kGemvRows) {
-    const int M = std::min(kGemvRows, rows - r0);
+  for (int r0 = 0; r0 < rows; r0 += launch_rows) {
+    const int M = std::min(launch_rows, rows - r0);
+    const bool pair = M > kGemvRows;  // two row groups (rotated launches: launch_rows is 16 otherwise)
     const GemvPlan pl = gemv_plan(k, n_total, M, K, cb, pre);
     const dim3 grid(n_total / 128, pl.splits);
     const void* xr = static_cast<const uint8_t*>(pre ? (const void*)xh : x) + (size_t)r0 * k * 2;
     void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
     bool ok = false;
+#define EXL3_GEMV_PAIR(NTV, PREV)                                                                                    \
+  ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, NTV, PREV, 2><<<grid, kGemvThreads, pl.lds, st>>>(      \
+      sa, xr, PREV ? 0 : (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows)));
+    if (pair) {  /* two row groups: the plan's LDS for 32 staged rows allows NT <= 32 */
+      if (pl.nt == 16 && pre)
+        EXL3_GEMV_PAIR(16, true)
+      else if (pl.nt == 16)
+        EXL3_GEMV_PAIR(16, false)
+      else if (pre)
+        EXL3_GEMV_PAIR(32, true)
+      else
+        EXL3_GEMV_PAIR(32, false)
+    }
+#undef EXL3_GEMV_PAIR
 #define EXL3_GEMV_LAUNCH(NTV)                                                                                        \
-  if (pl.nt == NTV) {                                                                                                \
+  if (!pair && pl.nt == NTV) {                                                                                       \
     if (pre) /* the plan gives at most 32 with prepared rows */                                                      \
       ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, (NTV > 32 ? 32 : NTV), true><<<grid, kGemvThreads,  \
                                                                                              pl.lds, st>>>(          \
@@ -696,8 +736,9 @@ extern "C" int exl3_had_out_into(const void* y, int rows, int n, const void* svh
 extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K) {
   (void)K;
   if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128 || n_total / 128 > kMaxCounters) return 0;
-  // launches take 16 rows at a time, then the remainder: the workspace holds either plan's partials
-  return counters_bytes(n_total) + gemv_partial_bytes(rows, k, n_total, K) + gemv_pre_bytes(rows, k, n_total);
+  // launches take 32 rows at a time (16 for exl3_gemm_rotated: its need is no larger), then the remainder: the
+  // workspace holds either plan's partials
+  return gemv_workspace_bytes(rows, k, n_total, K, kGemvPairRows);
 }
 
 extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards,
@@ -714,7 +755,7 @@ extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_linear: workspace %zu bytes, need %zu", workspace_bytes,
                  need);
   return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, workspace, y, y_bf16 != 0,
-                     as_stream(stream));
+                     as_stream(stream), kGemvPairRows);
 }
 
 extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook,
@@ -734,7 +775,8 @@ extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* tr
   sa.tn[0] = n / 16;
   sa.blk0[1] = n / 128;
   sa.count = 1;
-  return launch_gemv(sa, xh, false, false, rows, k, K, codebook, n, workspace, out, false, as_stream(stream));
+  return launch_gemv(sa, xh, false, false, rows, k, K, codebook, n, workspace, out, false, as_stream(stream),
+                     kGemvRows);
 }
 
 extern "C" size_t exl3_linear_noalloc_max_bytes(void) { return EXL3_NOALLOC_SCRATCH_BYTES; }
@@ -748,12 +790,13 @@ extern "C" int exl3_linear_noalloc(const void* x, int x_bf16, int rows, int k, c
   int n_total = 0;
   if (int rc = build_shards(shards_host, nshards, k, K, &sa, &n_total)) return rc;
   if (rows == 0) return EXL3_OK;
-  const size_t need = exl3_linear_workspace_bytes(rows, k, n_total, K);
+  // 16 rows per launch here (the scratch need of the two-row-group launches would be larger)
+  const size_t need = gemv_workspace_bytes(rows, k, n_total, K, kGemvRows);
   EXL3_CHECK_ARG(need <= (size_t)EXL3_NOALLOC_SCRATCH_BYTES,
                  "exl3_linear_noalloc: %d rows of %d -> %d need %zu bytes of scratch, the library holds %zu; use "
                  "exl3_linear with a workspace", rows, k, n_total, need, (size_t)EXL3_NOALLOC_SCRATCH_BYTES);
   hipStream_t st = as_stream(stream);
   void* ws = nullptr;
   if (int rc = scratch_of_current_device(st, &ws)) return rc;
-  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, ws, y, y_bf16 != 0, st);
+  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, ws, y, y_bf16 != 0, st, kGemvRows);
 }

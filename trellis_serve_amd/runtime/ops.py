@@ -3,12 +3,12 @@ row-count dispatch, dtype handling and output allocation live inside the op so a
 
 `torch.ops.exl3_mi355x.linear(x, trellis[], suh[], svh[], codebook)` -> y [..., sum n_s] in x's dtype.
 Dispatch (the reference's `_linear`, runtime/ops.py:62-126, with MI355X switch points):
-  rows < PREFILL_ROWS  -> fused decode-GEMV (exl3_linear, up to 16 rows per launch)
+  rows < PREFILL_ROWS  -> fused decode-GEMV (exl3_linear, up to 32 rows per launch)
   rows >= PREFILL_ROWS -> fused decode-GEMM (exl3_linear_prefill)
-PREFILL_ROWS comes from measured crossovers on the 27B shapes: the GEMV streams the weights once per 16 rows, the
-fused GEMM once for up to 256 rows.  Up to 32 rows (two GEMV passes) the GEMV is faster on every layer of the set;
-from three passes the GEMM is faster on the layer set as a whole (40 rows: gate/up 114 vs 95 us, down 74 vs 69,
-q/k/v 46 vs 46, o 42 vs 48; 64 rows: 148 vs 96, 101 vs 74, 62 vs 49, 57 vs 52).
+PREFILL_ROWS comes from measured crossovers on the 27B shapes: the GEMV streams the weights once per 32 rows (two
+16-row MFMA groups per decoded tile), the fused GEMM once for up to 256 rows.  Up to 48 rows the GEMV is faster on
+every layer of the set; at 64 rows (two GEMV launches) only gate/up is faster on the GEMM and the set as a whole is
+still faster on the GEMV (q/k/v 47.5 vs 50.3 us, o 42.0 vs 51.9, gate/up 102.5 vs 95.6, down 73.5 vs 74.9).
 """
 from __future__ import annotations
 
@@ -18,7 +18,7 @@ import torch
 
 from .. import ops as _kernels
 
-PREFILL_ROWS = int(os.environ.get("EXL3_MI355X_PREFILL_ROWS", "33"))
+PREFILL_ROWS = int(os.environ.get("EXL3_MI355X_PREFILL_ROWS", "65"))
 
 _lib = torch.library.Library("exl3_mi355x", "FRAGMENT")  # must stay alive at module scope
 
