@@ -150,11 +150,11 @@ def test_gemv_shards_of_uneven_widths(coracle, M, cb):
     assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 17, 24, 32, 45])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 17, 24, 32, 45, 64, 80])
 @pytest.mark.parametrize("K,cb", [(2, 1), (3, 1), (4, 0), (5, 2), (6, 1), (8, 0)])
 def test_linear_matches_float64_oracle(coracle, M, K, cb):
-    """Up to 16 rows one MFMA row group per decoded tile, 17-32 two groups in one launch (rows padded with zeros to
-    32), past 32 rows another launch for the rest."""
+    """Up to 16 rows one MFMA row group per decoded tile, 17-32 two groups and 33-64 four groups in one launch (rows
+    padded with zeros to a multiple of 16), past 64 rows another launch for the rest."""
     rng = np.random.default_rng(3000 + 100 * M + 10 * K + cb)
     k, n = 768, 640
     tr, suh, svh = _trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)
@@ -292,7 +292,7 @@ def test_workspace_shared_by_calls_of_different_shapes(coracle):
         assert nrel <= TOL and mrel <= TOL, (k, n, M, nrel, mrel)
 
 
-@pytest.mark.parametrize("rows", [17, 32])
+@pytest.mark.parametrize("rows", [17, 32, 50, 64])
 def test_two_row_groups_match_oracle_with_prepared_rows(coracle, rows):
     """Two 16-row groups share each decoded tile: at 17 rows every workgroup rotates its rows, at 32 rows (64 column
     blocks x 32 rows x 32 k-blocks) the input is rotated once per shard before the GEMV; both shards against the
@@ -312,3 +312,20 @@ def test_two_row_groups_match_oracle_with_prepared_rows(coracle, rows):
         assert nrel <= TOL and mrel <= TOL, (n, nrel, mrel)
         col += n
     assert torch.equal(_ops().linear(_dev(x), *args), y)
+
+
+@pytest.mark.parametrize("rows", [40, 64])
+def test_wide_layer_rows_past_32_take_two_group_launches(coracle, rows):
+    """A wide layer (256 column blocks) at 33-64 rows runs as launches of 32 rows with two row groups (four groups
+    would need more LDS than a launch gets by default); the first and last 1024 columns against the oracle."""
+    rng = np.random.default_rng(90 + rows)
+    k, n, K, cb = 2048, 32768, 3, 1
+    tr, suh, svh = _trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)
+    x = (rng.standard_normal((rows, k)) * 0.5).astype(np.float16)
+    y = _ops().linear(_dev(x), [_dev(tr)], [_dev(suh)], [_dev(svh)], cb).cpu().numpy()
+    for c0 in (0, n - 1024):
+        t = tr[:, c0 // 16:(c0 + 1024) // 16]
+        ref = orc.linear_forward(x, t, suh, svh[c0:c0 + 1024], K, cb, w_inner=c_reconstruct(coracle, t, K, cb),
+                                 dtype=np.float64)
+        nrel, mrel = _errs(y[:, c0:c0 + 1024], ref)
+        assert nrel <= TOL and mrel <= TOL, (c0, nrel, mrel)

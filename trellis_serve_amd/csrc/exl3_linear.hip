@@ -22,6 +22,7 @@ namespace exl3 {
 constexpr int kGemvWaves = 8;   // one wave per tile column: a workgroup covers one 128-column block
 constexpr int kGemvRows = 16;   // rows of one MFMA row group (the M of MFMA 16x16x16)
 constexpr int kGemvPairRows = 32;  // rows per launch with two row groups per decoded tile (gemv_kernel<..., P = 2>)
+constexpr int kGemvQuadRows = 64;  // rows per launch with four row groups (gemv_kernel<..., P = 4>)
 constexpr int kGemvMaxLds = 65536;  // dynamic LDS limit of a workgroup without opt-in
 
 struct ShardArgs {
@@ -224,8 +225,8 @@ __host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K, bool dup)
 
 // PRE: x is the rotated activations of every shard, [shards][pre_rows][k] in A-staging order (had_in_kernel<.., true>),
 // staged by plain 8-byte copies; else x is the input rows, rotated here (ROTATE) or taken as given
-// P = 2 (17-32 rows): every decoded tile feeds two 16-row MFMA groups (rounded fp16 weights, v_mfma 16x16x16): the
-// weights stream once for 32 rows instead of once per 16.  The staged rows are padded with zeros to 32.
+// P = 2 / 4 (17-32 / 33-64 rows): every decoded tile feeds P 16-row MFMA groups (rounded fp16 weights, v_mfma
+// 16x16x16): the weights stream once for 16 P rows instead of once per 16.  The staged rows are padded with zeros.
 template <int K, int CB, bool ROTATE, int NT, bool PRE = false, int P = 1>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
                                                              int M, int k, int splits, float* partial,
@@ -463,7 +464,7 @@ static int gemv_target_wgs(int M) {
 static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = false) {
   const int kb = k / 128, nblk = n_total / 128;
   const bool dup = cb != CB_MUL1 && M <= kGemvRows;
-  const int Ms = M <= kGemvRows ? M : kGemvPairRows;
+  const int Ms = M <= kGemvRows ? M : M <= kGemvPairRows ? kGemvPairRows : kGemvQuadRows;
   int nt = 16;
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
@@ -540,8 +541,20 @@ static bool gemv_pre(int rows, int k, int n_total) {
 // workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre]; the size does
 // not depend on the codebook (the largest plan of either staging form).  launch_rows: rows per launch, 16, or 32 where
 // two row groups share each decoded tile (exl3_linear)
+// Rows per launch: four row groups (64) only where the layer needs 16-tile-row splits for enough workgroups anyway
+// (narrow layers: q/k/v, o): there 64 staged rows fit the default LDS and one launch beats two.  Wider layers would
+// need 32-tile-row splits, whose 64 staged rows exceed that LDS (and the fp32 partials of 64 rows grow with the
+// splits): there 64 rows take two launches of two groups (measured at 64 rows: gate_up 102.5 us against 112.9 us with
+// one four-group launch, down 73.5 against 77.8; q/k/v 47.5 -> 39.2, o 42.0 -> 37.0 with it).
+static int gemv_launch_rows(int k, int n_total, int launch_rows) {
+  if (launch_rows < kGemvQuadRows) return launch_rows;
+  const int kb = k / 128, nblk = n_total / 128;
+  return (size_t)nblk * ((kb + 3) / 4) < (size_t)gemv_target_wgs(kGemvQuadRows) ? kGemvQuadRows : kGemvPairRows;
+}
+
 static size_t gemv_partial_bytes(int rows, int k, int n_total, int K, int launch_rows) {
   size_t need = 0;
+  launch_rows = gemv_launch_rows(k, n_total, launch_rows);
   for (int M : {std::min(rows, launch_rows), rows % launch_rows}) {
     if (M == 0) continue;
     for (int cb : {(int)CB_MCG, (int)CB_MUL1}) {
@@ -560,7 +573,7 @@ static size_t gemv_workspace_bytes(int rows, int k, int n_total, int K, int laun
          gemv_pre_bytes(rows, k, n_total);
 }
 
-// launch_rows: 32 (two row groups per decoded tile past 16 rows; rotated launches only) or 16
+// launch_rows: 64 (two or four row groups per decoded tile past 16 rows; rotated launches only) or 16
 static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_bf16, int rows, int k, int K, int cb,
                        int n_total, void* workspace, void* y, bool y_bf16, hipStream_t st, int launch_rows) {
   int* counters = static_cast<int*>(workspace);
@@ -576,9 +589,11 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
       had_in_shards_kernel<false><<<hgrid, 256, 0, st>>>(x, rows, k, sa, xh);
     EXL3_CHECK_LAUNCH();
   }
+  launch_rows = gemv_launch_rows(k, n_total, launch_rows);
   for (int r0 = 0; r0 < rows; r0 += launch_rows) {
     const int M = std::min(launch_rows, rows - r0);
-    const bool pair = M > kGemvRows;  // two row groups (rotated launches: launch_rows is 16 otherwise)
+    // two or four row groups per decoded tile (rotated launches only: launch_rows is 16 otherwise)
+    const bool quad = M > kGemvPairRows, pair = M > kGemvRows && !quad;
     const GemvPlan pl = gemv_plan(k, n_total, M, K, cb, pre);
     const dim3 grid(n_total / 128, pl.splits);
     const void* xr = static_cast<const uint8_t*>(pre ? (const void*)xh : x) + (size_t)r0 * k * 2;
@@ -598,8 +613,20 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
         EXL3_GEMV_PAIR(32, false)
     }
 #undef EXL3_GEMV_PAIR
+    // four row groups (narrow layers only, gemv_launch_rows): 64 staged rows at NT = 16 fit the default LDS
+#define EXL3_GEMV_QUAD(PREV)                                                                                         \
+  ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, 16, PREV, 4><<<grid, kGemvThreads, pl.lds, st>>>(       \
+      sa, xr, PREV ? 0 : (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows)));
+    if (quad) {
+      if (pl.nt != 16) return set_error(EXL3_ERR_INVALID, "four-group GEMV planned at NT = %d", pl.nt);
+      if (pre)
+        EXL3_GEMV_QUAD(true)
+      else
+        EXL3_GEMV_QUAD(false)
+    }
+#undef EXL3_GEMV_QUAD
 #define EXL3_GEMV_LAUNCH(NTV)                                                                                        \
-  if (!pair && pl.nt == NTV) {                                                                                       \
+  if (!pair && !quad && pl.nt == NTV) {                                                                              \
     if (pre) /* the plan gives at most 32 with prepared rows */                                                      \
       ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, (NTV > 32 ? 32 : NTV), true><<<grid, kGemvThreads,  \
                                                                                              pl.lds, st>>>(          \
@@ -736,9 +763,9 @@ extern "C" int exl3_had_out_into(const void* y, int rows, int n, const void* svh
 extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K) {
   (void)K;
   if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128 || n_total / 128 > kMaxCounters) return 0;
-  // launches take 32 rows at a time (16 for exl3_gemm_rotated: its need is no larger), then the remainder: the
+  // launches take 64 rows at a time (16 for exl3_gemm_rotated: its need is no larger), then the remainder: the
   // workspace holds either plan's partials
-  return gemv_workspace_bytes(rows, k, n_total, K, kGemvPairRows);
+  return gemv_workspace_bytes(rows, k, n_total, K, kGemvQuadRows);
 }
 
 extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards,
@@ -755,7 +782,7 @@ extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_linear: workspace %zu bytes, need %zu", workspace_bytes,
                  need);
   return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, workspace, y, y_bf16 != 0,
-                     as_stream(stream), kGemvPairRows);
+                     as_stream(stream), kGemvQuadRows);
 }
 
 extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook,

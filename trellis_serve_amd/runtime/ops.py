@@ -3,12 +3,12 @@ row-count dispatch, dtype handling and output allocation live inside the op so a
 
 `torch.ops.exl3_mi355x.linear(x, trellis[], suh[], svh[], codebook)` -> y [..., sum n_s] in x's dtype.
 Dispatch (the reference's `_linear`, runtime/ops.py:62-126, with MI355X switch points):
-  rows < PREFILL_ROWS  -> fused decode-GEMV (exl3_linear, up to 32 rows per launch)
+  rows < PREFILL_ROWS  -> fused decode-GEMV (exl3_linear, up to 64 rows per launch)
   rows >= PREFILL_ROWS -> fused decode-GEMM (exl3_linear_prefill)
-PREFILL_ROWS comes from measured crossovers on the 27B shapes: the GEMV streams the weights once per 32 rows (two
-16-row MFMA groups per decoded tile), the fused GEMM once for up to 256 rows.  Up to 48 rows the GEMV is faster on
-every layer of the set; at 64 rows (two GEMV launches) only gate/up is faster on the GEMM and the set as a whole is
-still faster on the GEMV (q/k/v 47.5 vs 50.3 us, o 42.0 vs 51.9, gate/up 102.5 vs 95.6, down 73.5 vs 74.9).
+PREFILL_ROWS comes from measured crossovers on the 27B shapes: the GEMV streams the weights once per 32 or 64 rows
+(two or four 16-row MFMA groups per decoded tile), the fused GEMM once for up to 256 rows.  At 64 rows the layer set
+is faster on the GEMV (q/k/v 39.3 vs 49.6 us, o 37.4 vs 51.6, gate/up 104.3 vs 96.5, down 74.3 vs 74.6), at 96 rows
+on the GEMM (382 vs 308 us).
 """
 from __future__ import annotations
 
