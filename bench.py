@@ -613,7 +613,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=1)
     ap.add_argument("--copies", type=int, default=5, help="rotating copies of the layer set (cold HBM)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--extra-rows", default="4,16", help="also report these M (comma list, '' for none)")
+    ap.add_argument("--extra-rows", default="4,16,32,64",
+                    help="also report these M (comma list, '' for none; past 16 rows the GEMV takes 2 or 4 row groups)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-secondary", action="store_true", help="skip the prefill / MoE / KV-attention lines")
     ap.add_argument("--probe", choices=["gate_up", "copy"], help=argparse.SUPPRESS)
