@@ -47,13 +47,13 @@ def _ws_ptr(kind):
     return _ops().workspace(torch.device("cuda"), 0, kind).data_ptr()
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 24, 48])   # one row group; two; four (a narrow layer)
 def test_linear_graph_after_reservation(M):
     ops = _ops()
     g = torch.Generator().manual_seed(31 + M)
     k, ns, K, cb = 2048, [1024, 512, 512], 3, 1
     trs, suhs, svhs = _group(g, k, ns, K)
-    ops.reserve_linear(torch.device("cuda"), 16, k, sum(ns), K)
+    ops.reserve_linear(torch.device("cuda"), max(16, M), k, sum(ns), K)
     ptr = _ws_ptr("linear")
     x = torch.randn((M, k), generator=g).half().cuda()
     out = torch.empty((M, sum(ns)), dtype=torch.float16, device="cuda")
@@ -61,7 +61,7 @@ def test_linear_graph_after_reservation(M):
     for i in range(4):
         other = torch.randn((16 if i % 2 else 7, k), generator=g).half().cuda()
         ops.linear(other, trs, suhs, svhs, cb)                       # eager, other shapes, same workspace
-        ops.linear(torch.randn((40, k), generator=g).half().cuda(), trs, suhs, svhs, cb)   # beyond the reservation
+        ops.linear(torch.randn((80, k), generator=g).half().cuda(), trs, suhs, svhs, cb)   # beyond the reservation
         x.copy_(torch.randn((M, k), generator=g).half().cuda())
         graph.replay()
         torch.cuda.synchronize()
