@@ -89,7 +89,8 @@ size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K);
 
 /* y[rows, sum n_s] = concat_s( Had128(Had128(x * suh_s) @ W_s) * svh_s ) with fp32 accumulation; fp16 output of
  * the GEMM, output transform as exl3_had_out_into.  x fp16|bf16 [rows, k]; y fp16|bf16 [rows, sum n_s].
- * All shards share K and codebook.  Replaces exl3_linear_marlin_out / exl3_linear_marlin_multi_out
+ * All shards share K and codebook.  One launch serves up to 64 rows (each decoded tile feeds 1, 2 or 4 16-row MFMA
+ * groups); more rows take more launches.  Replaces exl3_linear_marlin_out / exl3_linear_marlin_multi_out
  * (cuda/csrc/exl3_marlin.cu:489-527) behind torch.ops.sglang_exl3.linear (cuda/src/sglang_exl3/runtime/ops.py:133). */
 int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards, int K,
                 int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
@@ -102,10 +103,12 @@ int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int 
 
 /* Allocation-free form of exl3_linear.  No counterpart in the reference: it is for callers that cannot allocate or
  * pass device memory of their own (code under HIP-graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  Same arguments and results as exl3_linear without the workspace: the split counters and fp32
- * partials live in a scratch array of EXL3_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on
- * until the process ends.  It calls no allocating routine.  A call whose exl3_linear_workspace_bytes exceeds the
- * scratch returns EXL3_ERR_INVALID and launches nothing.  All calls on one GPU share its scratch: calls that overlap
+ * hipMalloc).  Same arguments as exl3_linear without the workspace, and the same results up to 16 rows (past 16 rows
+ * it runs one launch per 16 rows, where exl3_linear shares each decoded tile among up to 64 rows: the two then agree
+ * to rounding): the split counters and fp32 partials live in a scratch array of EXL3_NOALLOC_SCRATCH_BYTES that the
+ * library holds on every GPU it runs on until the process ends.  It calls no allocating routine.  A call whose
+ * workspace need (that of 16-row launches; exl3_linear_workspace_bytes up to 16 rows) exceeds the scratch returns
+ * EXL3_ERR_INVALID and launches nothing.  All calls on one GPU share its scratch: calls that overlap
  * in time on one GPU (several streams, several host threads without ordering) race and give wrong results; calls
  * ordered on one stream are safe, and each leaves the counters at zero for the next. */
 #define EXL3_NOALLOC_SCRATCH_BYTES (32u << 20)

@@ -392,48 +392,48 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   if (!last_flag) return;
 
   // last split of this column block: units (row m, 4-column group q); p-groups G share the splits p = g, g + G, ...
-  // and are combined in a fixed order.  Past 16 rows the units take two passes of 512.
+  // and are combined in a fixed order.  Past 16 rows the units take passes of 512 (16 rows each).
   float4_t* red = reinterpret_cast<float4_t*>(lds);  // reuse the LDS (>= 512 * 16 B reserved)
   const int tid = threadIdx.x;
   for (int u0 = 0; u0 < M * 32; u0 += kGemvThreads) {
-  const int units = min(M * 32 - u0, kGemvThreads);
-  const int G = max(1, kGemvThreads / units);
-  if (tid < units * G) {
-    const int unit = u0 + tid % units, gq = tid / units;
-    const int m = unit >> 5, q = unit & 31;
-    const int base = (m * n_total + col_blk + 4 * q) * 4;
-    const int pstride = M * n_total * 4;
-    // up to 8 loads in flight per round (only for splits that exist), summed in split order
-    float4_t a = {0.f, 0.f, 0.f, 0.f};
-    for (int p0 = gq; p0 < splits; p0 += 8 * G) {
-      float4_t v[8];
+    const int units = min(M * 32 - u0, kGemvThreads);
+    const int G = max(1, kGemvThreads / units);
+    if (tid < units * G) {
+      const int unit = u0 + tid % units, gq = tid / units;
+      const int m = unit >> 5, q = unit & 31;
+      const int base = (m * n_total + col_blk + 4 * q) * 4;
+      const int pstride = M * n_total * 4;
+      // up to 8 loads in flight per round (only for splits that exist), summed in split order
+      float4_t a = {0.f, 0.f, 0.f, 0.f};
+      for (int p0 = gq; p0 < splits; p0 += 8 * G) {
+        float4_t v[8];
 #pragma unroll
-      for (int i = 0; i < 8; i++)
-        v[i] = p0 + i * G < splits ? __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                      prsrc, base + (p0 + i * G) * pstride, 0,
-                                                                      kCoherentDevice))
-                                   : float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 8; i++)
+          v[i] = p0 + i * G < splits ? __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                        prsrc, base + (p0 + i * G) * pstride, 0,
+                                                                        kCoherentDevice))
+                                     : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 8; i++)
-        if (p0 + i * G < splits) a += v[i];
+        for (int i = 0; i < 8; i++)
+          if (p0 + i * G < splits) a += v[i];
+      }
+      red[gq * units + unit - u0] = a;
     }
-    red[gq * units + unit - u0] = a;
-  }
-  __syncthreads();
-  if (tid < units) {
-    float4_t a = red[tid];
-    for (int gq = 1; gq < G; gq++) a += red[gq * units + tid];
-    const int m = (u0 + tid) >> 5, q = tid & 31;
-    _Float16 h[4] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
-    const int col = col_blk + 4 * q;
-    if constexpr (ROTATE) had_out_4(h, sh.svh + (col - sh.col0));
-    uint16_t* yrow = static_cast<uint16_t*>(y) + (size_t)m * n_total;
-    if (y_bf16)
-      store_4<true>(yrow, col, h);
-    else
-      store_4<false>(yrow, col, h);
-  }
-  __syncthreads();  // the next pass reuses red
+    __syncthreads();
+    if (tid < units) {
+      float4_t a = red[tid];
+      for (int gq = 1; gq < G; gq++) a += red[gq * units + tid];
+      const int m = (u0 + tid) >> 5, q = tid & 31;
+      _Float16 h[4] = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
+      const int col = col_blk + 4 * q;
+      if constexpr (ROTATE) had_out_4(h, sh.svh + (col - sh.col0));
+      uint16_t* yrow = static_cast<uint16_t*>(y) + (size_t)m * n_total;
+      if (y_bf16)
+        store_4<true>(yrow, col, h);
+      else
+        store_4<false>(yrow, col, h);
+    }
+    __syncthreads();  // the next pass reuses red
   }
   if (tid == 0) __hip_atomic_store(&counters[blk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -538,9 +538,6 @@ static bool gemv_pre(int rows, int k, int n_total) {
   return rows >= kGemvPreRows && (size_t)(n_total / 128) * rows * (k / 128) >= kGemvPreUnits;
 }
 
-// workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre]; the size does
-// not depend on the codebook (the largest plan of either staging form).  launch_rows: rows per launch, 16, or 32 where
-// two row groups share each decoded tile (exl3_linear)
 // Rows per launch: four row groups (64) only where the layer needs 16-tile-row splits for enough workgroups anyway
 // (narrow layers: q/k/v, o): there 64 staged rows fit the default LDS and one launch beats two.  Wider layers would
 // need 32-tile-row splits, whose 64 staged rows exceed that LDS (and the fp32 partials of 64 rows grow with the
@@ -552,6 +549,9 @@ static int gemv_launch_rows(int k, int n_total, int launch_rows) {
   return (size_t)nblk * ((kb + 3) / 4) < (size_t)gemv_target_wgs(kGemvQuadRows) ? kGemvQuadRows : kGemvPairRows;
 }
 
+// workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre]; the size does
+// not depend on the codebook (the largest plan of either staging form).  launch_rows: the caller's rows per launch,
+// 16, or 64 where row groups share each decoded tile (exl3_linear; gemv_launch_rows may lower it to 32)
 static size_t gemv_partial_bytes(int rows, int k, int n_total, int K, int launch_rows) {
   size_t need = 0;
   launch_rows = gemv_launch_rows(k, n_total, launch_rows);
