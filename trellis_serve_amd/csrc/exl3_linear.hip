@@ -448,14 +448,18 @@ struct GemvPlan {
   size_t lds;
 };
 
-// the workgroup target: 1536 below 8 rows; from 8 rows, where every split's fp32 partial of M rows is written and
-// read again and the last split's reduce reads all of them, half that (measured at 16 rows: down 31.5 -> 29.0 us)
+// the workgroup target from 8 rows, where every split's fp32 partial of M rows is written and read again and the
+// last split's reduce reads all of them (measured at 16 rows: down 31.5 -> 29.0 us against 1536); fewer rows take
+// the equal-split rule of gemv_plan
+constexpr int kGemvFewRows = 8;
+constexpr int kGemvFewRowWgs = 512;
 static int gemv_target_wgs(int M) {
   static const int env = [] {
     const char* e = getenv("EXL3_GEMV_TARGET_WGS");
     return e ? std::max(1, atoi(e)) : 0;
   }();
-  return env ? env : M >= 8 ? 768 : 1536;
+  (void)M;
+  return env ? env : 768;
 }
 
 // pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there.
@@ -466,6 +470,21 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = f
   const bool dup = cb != CB_MUL1 && M <= kGemvRows;
   const int Ms = M <= kGemvRows ? M : M <= kGemvPairRows ? kGemvPairRows : kGemvQuadRows;
   int nt = 16;
+  if (M < kGemvFewRows) {
+    // below 8 rows: the longest split of at most 40 tile rows that cuts k into equal splits (at most 2 % of the last
+    // one empty) and still gives >= 512 workgroups.  Measured at one row, each layer against its 16 / 32 tile rows
+    // of a 1536-workgroup target (same call): down 21.3 -> 18.6 us (32), q/k/v 12.9 -> 11.9 (40), o 11.7 -> 11.0
+    // (24), gate_up 33.7 -> 33.5 (40); 48-64 tile rows were no faster anywhere and slower on q/k/v and gate_up.
+    for (int cand : {40, 32, 24}) {
+      const int nbc = cand / 8, splits = (kb + nbc - 1) / nbc;
+      if (splits * nbc * 50 <= kb * 51 && (size_t)nblk * splits >= kGemvFewRowWgs &&
+          gemv_lds_bytes(Ms, cand, K, dup) <= kGemvMaxLds) {
+        nt = cand;
+        break;
+      }
+    }
+    return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(Ms, nt, K, dup)};
+  }
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
     if (pre && cand > 32) continue;
@@ -642,6 +661,19 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
     EXL3_GEMV_LAUNCH(32)
     EXL3_GEMV_LAUNCH(64)
 #undef EXL3_GEMV_LAUNCH
+    // 24 and 40 tile rows: below 8 rows only, so never with prepared rows or row groups
+#define EXL3_GEMV_FEW(NTV)                                                                                           \
+  if (!pair && !quad && !pre && pl.nt == NTV) {                                                                      \
+    if (rotate)                                                                                                      \
+      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, NTV><<<grid, kGemvThreads, pl.lds, st>>>(           \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+    else                                                                                                             \
+      ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false, NTV><<<grid, kGemvThreads, pl.lds, st>>>(          \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+  }
+    EXL3_GEMV_FEW(24)
+    EXL3_GEMV_FEW(40)
+#undef EXL3_GEMV_FEW
     if (!ok) return set_error(EXL3_ERR_INVALID, "unsupported K = %d / codebook = %d", K, cb);
     EXL3_CHECK_LAUNCH();
   }
