@@ -448,17 +448,15 @@ struct GemvPlan {
   size_t lds;
 };
 
-// the workgroup target from 8 rows, where every split's fp32 partial of M rows is written and read again and the
-// last split's reduce reads all of them (measured at 16 rows: down 31.5 -> 29.0 us against 1536); fewer rows take
-// the equal-split rule of gemv_plan
-constexpr int kGemvFewRows = 8;
-constexpr int kGemvFewRowWgs = 512;
-static int gemv_target_wgs(int M) {
+// the workgroup target of the two- and four-group launches (17-64 rows), where every split's fp32 partial of M rows
+// is written and read again and the last split's reduce reads all of them; one row group takes the equal-split rule
+// of gemv_plan and its own minimum
+constexpr int kGemvOneGroupWgs = 448;
+static int gemv_target_wgs() {
   static const int env = [] {
     const char* e = getenv("EXL3_GEMV_TARGET_WGS");
     return e ? std::max(1, atoi(e)) : 0;
   }();
-  (void)M;
   return env ? env : 768;
 }
 
@@ -470,14 +468,16 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = f
   const bool dup = cb != CB_MUL1 && M <= kGemvRows;
   const int Ms = M <= kGemvRows ? M : M <= kGemvPairRows ? kGemvPairRows : kGemvQuadRows;
   int nt = 16;
-  if (M < kGemvFewRows) {
-    // below 8 rows: the longest split of at most 40 tile rows that cuts k into equal splits (at most 2 % of the last
-    // one empty) and still gives >= 512 workgroups.  Measured at one row, each layer against its 16 / 32 tile rows
-    // of a 1536-workgroup target (same call): down 21.3 -> 18.6 us (32), q/k/v 12.9 -> 11.9 (40), o 11.7 -> 11.0
-    // (24), gate_up 33.7 -> 33.5 (40); 48-64 tile rows were no faster anywhere and slower on q/k/v and gate_up.
+  if (M <= kGemvRows) {
+    // one row group: the longest split of at most 40 tile rows (prepared rows: 32) that cuts k into equal splits (at
+    // most 2 % of the last one empty) and still gives >= 448 workgroups.  Measured against the earlier plan (16 / 32
+    // tile rows for >= 1536 workgroups below 8 rows, >= 768 from 8; same call): one row down 21.3 -> 18.6 us (32),
+    // q/k/v 12.9 -> 11.9 (40), o 11.7 -> 11.0 (32), gate_up 33.7 -> 33.5 (40); 16 rows q/k/v 18.4 -> 16.7 (40),
+    // o 16.2 -> 15.4 (32); 48-64 tile rows were no faster anywhere and slower on q/k/v and gate_up.
     for (int cand : {40, 32, 24}) {
+      if (pre && cand != 32) continue;
       const int nbc = cand / 8, splits = (kb + nbc - 1) / nbc;
-      if (splits * nbc * 50 <= kb * 51 && (size_t)nblk * splits >= kGemvFewRowWgs &&
+      if (splits * nbc * 50 <= kb * 51 && (size_t)nblk * splits >= kGemvOneGroupWgs &&
           gemv_lds_bytes(Ms, cand, K, dup) <= kGemvMaxLds) {
         nt = cand;
         break;
@@ -488,7 +488,7 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = f
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
     if (pre && cand > 32) continue;
-    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs(M) && gemv_lds_bytes(Ms, cand, K, dup) <= kGemvMaxLds) {
+    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs() && gemv_lds_bytes(Ms, cand, K, dup) <= kGemvMaxLds) {
       nt = cand;
       break;
     }
@@ -565,7 +565,7 @@ static bool gemv_pre(int rows, int k, int n_total) {
 static int gemv_launch_rows(int k, int n_total, int launch_rows) {
   if (launch_rows < kGemvQuadRows) return launch_rows;
   const int kb = k / 128, nblk = n_total / 128;
-  return (size_t)nblk * ((kb + 3) / 4) < (size_t)gemv_target_wgs(kGemvQuadRows) ? kGemvQuadRows : kGemvPairRows;
+  return (size_t)nblk * ((kb + 3) / 4) < (size_t)gemv_target_wgs() ? kGemvQuadRows : kGemvPairRows;
 }
 
 // workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre]; the size does
@@ -661,7 +661,7 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
     EXL3_GEMV_LAUNCH(32)
     EXL3_GEMV_LAUNCH(64)
 #undef EXL3_GEMV_LAUNCH
-    // 24 and 40 tile rows: below 8 rows only, so never with prepared rows or row groups
+    // 24 and 40 tile rows: one row group without prepared rows only
 #define EXL3_GEMV_FEW(NTV)                                                                                           \
   if (!pair && !quad && !pre && pl.nt == NTV) {                                                                      \
     if (rotate)                                                                                                      \
