@@ -80,11 +80,19 @@ def _capture(torch, fn):
     return g
 
 
+# steps per graph: a serving engine replays one graph per decode step holding every layer (hundreds of launches), so
+# the few microseconds between two replays are spread over many launches there; 20 layer sets per graph keep that
+# share near what serving pays (5 per graph: +1.7 us per step)
+GRAPH_STEPS = 20
+
+
 def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int):
-    """One graph holds R steps (step r: the 4 fused linears on rotating copy r).  Replays it ceil(steps / R) times
-    after ceil(warmup / R) untimed replays; returns (steps timed, ms per step, per-layer us per launch).  Per-layer
-    times come from a graph of R launches of that layer alone, timed the same way (same warmup)."""
+    """One graph holds S steps, rounds of the R copies (step i: the 4 fused linears on copy i mod R), S = R x up to
+    GRAPH_STEPS // R rounds, no more than the steps asked for allow.  Replays it ceil(steps / S) times after
+    ceil(warmup / S) untimed replays; returns (steps timed, ms per step, per-layer us per launch).  Per-layer times
+    come from a graph of S launches of that layer alone, timed the same way (same warmup)."""
     R = len(sets)
+    S = R * max(1, min(GRAPH_STEPS // R, steps // R))
     names = list(LAYERS)
     outs = {nm: torch.empty((xs[nm].shape[0], sum(LAYERS[nm][1])), dtype=torch.float16, device=xs[nm].device)
             for nm in names}
@@ -107,15 +115,16 @@ def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)
 
-    g_all = _capture(torch, lambda: run(range(R), names))
-    reps = -(-steps // R)
-    total = timed(g_all, reps, -(-warmup // R))
+    order = [i % R for i in range(S)]
+    g_all = _capture(torch, lambda: run(order, names))
+    reps = -(-steps // S)
+    total = timed(g_all, reps, -(-warmup // S))
     per_layer = {}
     for nm in names:
-        g = _capture(torch, lambda nm=nm: run(range(R), [nm]))
+        g = _capture(torch, lambda nm=nm: run(order, [nm]))
         lreps = max(4, reps // 2)
-        per_layer[nm] = timed(g, lreps, -(-warmup // R)) / (lreps * R)
-    return reps * R, total / (reps * R), per_layer
+        per_layer[nm] = timed(g, lreps, -(-warmup // S)) / (lreps * S)
+    return reps * S, total / (reps * S), per_layer
 
 
 def _cpu_threads() -> int:
