@@ -46,12 +46,22 @@ struct ShardView {
   int tn, col0, blk0;
 };
 
+// Every field of every shard is read into scalar registers before the compares (the empty asm statements take them
+// as operands): left to itself the compiler loads only the chosen shard's fields, after the compares, which puts two
+// or three dependent rounds of kernarg loads in front of the first memory request of every workgroup.
 __device__ __forceinline__ ShardView shard_of_block(const ShardArgs& sa, int blk) {
-  ShardView v{sa.trellis[0], sa.suh[0], sa.svh[0], sa.tn[0], sa.col0[0], sa.blk0[0]};
+  ShardView f[EXL3_MAX_SHARDS];
+#pragma unroll
+  for (int i = 0; i < EXL3_MAX_SHARDS; i++) {
+    f[i] = ShardView{sa.trellis[i], sa.suh[i], sa.svh[i], sa.tn[i], sa.col0[i], sa.blk0[i]};
+    asm volatile("" ::"s"(f[i].trellis), "s"(f[i].suh), "s"(f[i].svh), "s"(f[i].tn), "s"(f[i].col0), "s"(f[i].blk0));
+  }
+  const int count = sa.count;
+  asm volatile("" ::"s"(count));
+  ShardView v = f[0];
 #pragma unroll
   for (int i = 1; i < EXL3_MAX_SHARDS; i++)
-    if (i < sa.count && blk >= sa.blk0[i])
-      v = ShardView{sa.trellis[i], sa.suh[i], sa.svh[i], sa.tn[i], sa.col0[i], sa.blk0[i]};
+    if (i < count && blk >= f[i].blk0) v = f[i];
   return v;
 }
 
@@ -240,6 +250,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
   const int blk = blockIdx.x, split = blockIdx.y;
+  asm volatile("" ::"s"(x), "s"(M), "s"(k), "s"(x_bf16));  // with the shard fields: one round of kernarg loads
   const ShardView sh = shard_of_block(sa, blk);
   const int kb0 = split * NB;
   const int nb = min(k >> 7, kb0 + NB) - kb0;  // blocks of this split holding data (1..NB)
