@@ -51,7 +51,8 @@ struct MoeArgs {
   const int* active;       // [E]: active experts, ascending
   const int* lists;        // [E][slots]
   const int* topk_ids;     // [slots]: read directly in slot mode and by the route+prep launch
-  int slot_mode;           // 1: one workgroup row per slot, no routing launch (a single token: its top-k experts)
+  int slot_mode;           // 1: one workgroup row per slot, no routing launch (a single token: its top-k experts);
+                           // the kernels take it from their PRE = false instance
   // rotated activations written once per slot, each 128-block in the staging order of a_slot: gate/up inputs
   // [2][slots][H] (moe_route_prep_kernel) and down inputs [slots][I] (the gate/up reducer), both for several tokens
   const uint16_t* pre_in;
@@ -220,10 +221,17 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
 
   // expert and its slots: routed mode -- grid row = active expert, its slot list from the routing launch; slot mode
   // -- grid row = slot, one slot, its expert read from topk_ids (split counters then index slots, so repeated experts
-  // in one token are still right)
+  // in one token are still right).  Slot mode is the launch without prepared rows (PRE = false), a compile-time
+  // choice, so the single-token kernel has no routed-mode argument loads ahead of its expert id, and the empty asm
+  // (taking the arguments as operands) puts every argument load into the round that fetches topk_ids.
   int e, n_e, ctr_row;
   const int* list;
-  if (a.slot_mode) {
+  if constexpr (!PRE)
+    asm volatile("" ::"s"(a.tr[0]), "s"(a.tr[1]), "s"(a.tr[2]), "s"(a.suh[0]), "s"(a.suh[1]), "s"(a.suh[2]),
+                 "s"(a.svh[0]), "s"(a.svh[1]), "s"(a.svh[2]), "s"(a.E), "s"(a.H), "s"(a.I), "s"(a.top_k),
+                 "s"(a.topk_ids), "s"(x), "s"(x_bf16), "s"(gu), "s"(dn), "s"(partial), "s"(counters), "s"(splits),
+                 "s"(chunks));
+  if constexpr (!PRE) {
     e = a.topk_ids[blockIdx.y];
     if (e < 0 || e >= a.E) return;
     n_e = 1;
@@ -236,7 +244,7 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
     list = a.lists + (size_t)e * a.slots;
     ctr_row = e;
   }
-  auto slot_at = [&](int idx) { return a.slot_mode ? (int)blockIdx.y : list[idx]; };
+  auto slot_at = [&](int idx) { return !PRE ? (int)blockIdx.y : list[idx]; };
   const int cb = blockIdx.x, sp = blockIdx.z;
   const int k = PHASE ? a.I : a.H;            // input width
   const int n_out = PHASE ? a.H : 2 * a.I;    // output row width (g|u for gate/up)
@@ -245,9 +253,9 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
   const int cbl = PHASE ? cb : cb - (sh ? a.I / 128 : 0);  // column block inside the shard
   const int tn = n_sh / 16;
   const int mat_bytes = (k >> 4) * tn * 32 * K;
-  const uint32_t* trellis = a.tr[sh] + (size_t)e * (mat_bytes / 4);
-  const uint16_t* suh = a.suh[sh] + (size_t)e * k;
-  const uint16_t* svh = a.svh[sh] + (size_t)e * n_sh;
+  const uint32_t* trellis = (sh == 0 ? a.tr[0] : sh == 1 ? a.tr[1] : a.tr[2]) + (size_t)e * (mat_bytes / 4);
+  const uint16_t* suh = (sh == 0 ? a.suh[0] : sh == 1 ? a.suh[1] : a.suh[2]) + (size_t)e * k;
+  const uint16_t* svh = (sh == 0 ? a.svh[0] : sh == 1 ? a.svh[1] : a.svh[2]) + (size_t)e * n_sh;
   const uint16_t* pre = PRE ? (PHASE ? a.pre_dn : a.pre_in + (size_t)sh * a.slots * k) : nullptr;
   // this split's k range: `chunks` chunks of NB 128-row blocks, from chunk sp * chunks (the last split may hold fewer)
   const int kblocks = k >> 7;
