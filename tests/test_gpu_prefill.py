@@ -127,3 +127,28 @@ def test_prefill_few_rows_many_contributors(coracle, M, n):
     assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
     for _ in range(2):
         assert torch.equal(_ops().linear_prefill(_dev(x), *args), y)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("rows,k,ns", [(37, 512, (256,)), (2200, 640, (512, 128, 256)), (8200, 2048, (128,))])
+def test_prefill_rotation_layouts_bit_identical(bf16, rows, k, ns):
+    """The input rotation has two kernels: 16 lanes per 128-value unit with 16-byte loads (x and every suh 16-byte
+    aligned) and 32 lanes with 8-byte loads (otherwise).  Both run the butterfly's stages in the same order on the
+    same pairs, so the whole prefill output must be bit-identical.  An input viewed 8 bytes into a buffer takes the
+    second kernel.  The shapes reach 1, 2 and 4 units per lane group of the first (below 2^15, from 2^15, from 2^17
+    units)."""
+    rng = np.random.default_rng(9100 + rows + int(bf16))
+    K, cb = 3, 1
+    cases = [_case(rng, k, n, K) for n in ns]
+    args = ([_dev(c[0]) for c in cases], [_dev(c[1]) for c in cases], [_dev(c[2]) for c in cases], cb)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    x = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float32) * 0.5).to(dt).cuda()
+    buf = torch.empty(rows * k + 8, dtype=dt, device="cuda")
+    x_off = buf[4:4 + rows * k].view(rows, k)
+    x_off.copy_(x)
+    assert x.data_ptr() % 16 == 0 and x_off.data_ptr() % 16 == 8
+    y16 = _ops().linear_prefill(x, *args)
+    y8 = _ops().linear_prefill(x_off, *args)
+    torch.cuda.synchronize()
+    assert torch.equal(y16.view(torch.int16), y8.view(torch.int16))
+    assert torch.isfinite(y16.float()).all()

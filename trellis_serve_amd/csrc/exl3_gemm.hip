@@ -102,6 +102,84 @@ struct ShardSuh {
   const uint16_t* suh[EXL3_MAX_SHARDS];
 };
 
+// Shard s of a rotation unit and its suh (a select over the few shards keeps the pointer in scalar registers)
+__device__ __forceinline__ const uint16_t* unit_suh(const ShardSuh& su_all, int s) {
+  return s == 0 ? su_all.suh[0] : s == 1 ? su_all.suh[1] : s == 2 ? su_all.suh[2] : su_all.suh[3];
+}
+
+// The same rotation with 16 lanes per 128-value (row, block) unit: lane t holds positions 8t .. 8t+7, read with one
+// 16-byte load of x and one of suh (x and every suh 16-byte aligned; the host checks).  The butterfly runs the stages
+// of had128_x4 in the same order on the same pairs -- h = 1, 2, 4 inside the lane (h = 4 was the lane-xor-1 stage
+// of the 4-per-lane form: lower = a + b, upper = a - b, the same sums), then lane xor 1, 2, 4, 8 for h = 8 .. 64 --
+// so the rotated values are bit-identical.  Fragment order: lane t (a = t & 3) holds, per q = 0..3, the slot pair
+// (q, tr = a >> 1, e = 2 (a & 1) + 0/1); lanes a and a ^ 1 swap two dwords (DPP) so that each stores two 8-byte
+// slot groups (q, tr) whole.  A 16-lane group takes U consecutive units with all loads issued first.
+template <bool X_BF16, int U>
+__global__ __launch_bounds__(256) void had_in_frag16_kernel(const void* __restrict__ x, int rows, int k,
+                                                            ShardSuh su_all, int shards, uint16_t* __restrict__ xh) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const int kb = k >> 7;
+  const int units = shards * rows * kb;
+  const int u0 = (blockIdx.x * 16 + (threadIdx.x >> 4)) * U;
+  if (u0 >= units) return;  // the whole 16-lane row: the DPP stages below stay inside rows of 16 lanes
+  const int t = threadIdx.x & 15;
+  u32x4_t xv[U], sv[U];
+#pragma unroll
+  for (int j = 0; j < U; j++) {
+    const int u = min(u0 + j, units - 1);  // past the end: a repeat of the last unit, not stored
+    const int s = u / (rows * kb), rem = u - s * rows * kb, r = rem / kb, b = rem - r * kb;
+    const int kk = b * 128 + 8 * t;
+    xv[j] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + (size_t)r * k + kk);
+    sv[j] = *reinterpret_cast<const u32x4_t*>(unit_suh(su_all, s) + kk);
+  }
+#pragma unroll
+  for (int j = 0; j < U; j++) {
+    const int u = u0 + j;
+    if (u >= units) break;
+    const int s = u / (rows * kb), rem = u - s * rows * kb, r = rem / kb, b = rem - r * kb;
+    const half8_t sc = __builtin_bit_cast(half8_t, sv[j]);
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t w = xv[j][i >> 1];
+      const uint16_t raw = (uint16_t)((i & 1) ? w >> 16 : w & 0xFFFF);
+      const _Float16 v = X_BF16 ? (_Float16)bf16_to_f32(raw) : __builtin_bit_cast(_Float16, raw);
+      f[i] = (float)(_Float16)(v * sc[i]);
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        if (!(i & h)) {
+          const float a = f[i], bb = f[i + h];
+          f[i] = a + bb;
+          f[i + h] = a - bb;
+        }
+    had_stage<1>(f[0], f[1], f[2], f[3]);
+    had_stage<1>(f[4], f[5], f[6], f[7]);
+    had_stage<2>(f[0], f[1], f[2], f[3]);
+    had_stage<2>(f[4], f[5], f[6], f[7]);
+    had_stage<4>(f[0], f[1], f[2], f[3]);
+    had_stage<4>(f[4], f[5], f[6], f[7]);
+    had_stage<8>(f[0], f[1], f[2], f[3]);
+    had_stage<8>(f[4], f[5], f[6], f[7]);
+    uint32_t d[4];  // d[q] = fp16 pair (positions 2q, 2q+1 of the lane)
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      d[q] = __builtin_bit_cast(uint32_t, half2_t{had_scale_f16(f[2 * q]), had_scale_f16(f[2 * q + 1])});
+    const bool low = (t & 1) == 0;
+    // lane a (even) stores q = 0, 2 as [own, partner's]; lane a + 1 stores q = 1, 3 as [partner's, own]
+    const uint32_t g0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)(low ? d[1] : d[0]), 0xB1, 0xF, 0xF, false);
+    const uint32_t g1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)(low ? d[3] : d[2]), 0xB1, 0xF, 0xF, false);
+    const uint2_t o0 = low ? uint2_t{d[0], g0} : uint2_t{g0, d[1]};
+    const uint2_t o1 = low ? uint2_t{d[2], g1} : uint2_t{g1, d[3]};
+    const int a = t & 3, blk32 = t >> 2, tr = a >> 1, q0 = low ? 0 : 1;
+    uint16_t* dst = xh + (size_t)s * rows * k + ((size_t)(b * 4 + blk32) * rows + r) * 32 + tr * 4;
+    *reinterpret_cast<uint2_t*>(dst + q0 * 8) = o0;
+    *reinterpret_cast<uint2_t*>(dst + (q0 + 2) * 8) = o1;
+  }
+}
+
 // rotated activations in fragment order: xh_f[s*rows + r][k] for shard s (see the header comment).  A half-wave
 // takes U consecutive 128-value (row, block) units, issues all their loads first (one round of load latency per
 // half-wave instead of one per unit), then rotates and stores each; lane t holds positions 4t .. 4t+3 of a block.
@@ -120,7 +198,7 @@ __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict
     const int u = min(u0 + j, units - 1);  // past the end: a repeat of the last unit, not stored
     const int s = u / (rows * kb), rem = u - s * rows * kb, r = rem / kb, b = rem - r * kb;
     const int kk = b * 128 + 4 * t;
-    const uint16_t* su = s == 0 ? su_all.suh[0] : s == 1 ? su_all.suh[1] : s == 2 ? su_all.suh[2] : su_all.suh[3];
+    const uint16_t* su = unit_suh(su_all, s);
     xv[j] = *reinterpret_cast<const uint2_t*>(static_cast<const uint16_t*>(x) + (size_t)r * k + kk);
     sv[j] = *reinterpret_cast<const uint2_t*>(su + kk);
   }
@@ -591,11 +669,23 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   ShardSuh su{};
   for (int s = 0; s < nshards; s++) su.suh[s] = static_cast<const uint16_t*>(shards_host[s].suh);
   const size_t hunits = (size_t)nshards * rows * (k / 128);
-  const int hu = hunits >= (1u << 17) ? 4 : 1;
-  const dim3 hgrid((unsigned)((hunits + 8 * hu - 1) / (8 * hu)));
-  auto frag = x_bf16 ? (hu == 4 ? had_in_frag_kernel<true, 4> : had_in_frag_kernel<true, 1>)
-                     : (hu == 4 ? had_in_frag_kernel<false, 4> : had_in_frag_kernel<false, 1>);
-  frag<<<hgrid, 256, 0, st>>>(x, rows, k, su, nshards, xh);
+  bool aligned16 = ((uintptr_t)x & 15) == 0;
+  for (int s = 0; s < nshards; s++) aligned16 = aligned16 && ((uintptr_t)su.suh[s] & 15) == 0;
+  if (aligned16) {
+    const int hu = hunits >= (1u << 17) ? 4 : hunits >= (1u << 15) ? 2 : 1;
+    const dim3 hgrid((unsigned)((hunits + 16 * hu - 1) / (16 * hu)));
+    auto frag = x_bf16 ? (hu == 4 ? had_in_frag16_kernel<true, 4> : hu == 2 ? had_in_frag16_kernel<true, 2>
+                                                                            : had_in_frag16_kernel<true, 1>)
+                       : (hu == 4 ? had_in_frag16_kernel<false, 4> : hu == 2 ? had_in_frag16_kernel<false, 2>
+                                                                             : had_in_frag16_kernel<false, 1>);
+    frag<<<hgrid, 256, 0, st>>>(x, rows, k, su, nshards, xh);
+  } else {
+    const int hu = hunits >= (1u << 17) ? 4 : 1;
+    const dim3 hgrid((unsigned)((hunits + 8 * hu - 1) / (8 * hu)));
+    auto frag = x_bf16 ? (hu == 4 ? had_in_frag_kernel<true, 4> : had_in_frag_kernel<true, 1>)
+                       : (hu == 4 ? had_in_frag_kernel<false, 4> : had_in_frag_kernel<false, 1>);
+    frag<<<hgrid, 256, 0, st>>>(x, rows, k, su, nshards, xh);
+  }
   EXL3_CHECK_LAUNCH();
   const dim3 grid((unsigned)(L.groups + L.tiles - L.sk_tiles));
   bool ok;
