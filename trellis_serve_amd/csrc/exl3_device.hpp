@@ -107,20 +107,30 @@ __device__ __forceinline__ uint32_t cb_hash_masked(uint32_t s) {
 // fp16 pair [lo + hi of y0, lo + hi of y1], each sum rounded once (v_add_f16 == __hadd).
 #ifndef EXL3_PERM_HALF_SUMS
 // SDWA reads the halves in place and writes the second sum into the upper half: one VALU op per weight.  The
-// compiler cannot see the VGPR writes inside the asm, so the block ends with the wait states an MFMA needs before
-// reading a VGPR a VALU op wrote (without them the next MFMA has read a stale B operand).
+// compiler cannot see the VGPR writes inside the asm, so where the sums feed an MFMA (MFMA_NEXT) the block ends with
+// the wait states an MFMA needs before reading a VGPR a VALU op wrote (without them the next MFMA has read a stale B
+// operand).  Sums that are stored (to LDS or memory) need no wait states: the store waits for its data like any
+// other instruction (prefill GEMM without them: 2 % faster, same results).
+template <bool MFMA_NEXT = true>
 __device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
   uint32_t r;
-  asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-      "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
-      "s_nop 2"
-      : "=&v"(r)
-      : "v"(y0), "v"(y1));
+  if constexpr (MFMA_NEXT)
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "s_nop 2"
+        : "=&v"(r)
+        : "v"(y0), "v"(y1));
+  else
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %0, %2, %2 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=&v"(r)
+        : "v"(y0), "v"(y1));
   return r;
 }
 #else
 // Two v_perm gather the low and the high halves, one v_pk_add_f16 adds them: 1.5 VALU ops per weight, all visible
 // to the compiler's hazard tracking.
+template <bool MFMA_NEXT = true>
 __device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
   const uint32_t lo = __builtin_amdgcn_perm(y1, y0, 0x05040100u);  // [y0.lo, y1.lo]
   const uint32_t hi = __builtin_amdgcn_perm(y1, y0, 0x07060302u);  // [y0.hi, y1.hi]
@@ -129,7 +139,7 @@ __device__ __forceinline__ uint32_t half_sums(uint32_t y0, uint32_t y1) {
 #endif
 
 // two states -> packed fp16 [v(sa), v(sb)], bit-exact with codebook_lut
-template <int CB>
+template <int CB, bool MFMA_NEXT = true>
 __device__ __forceinline__ uint32_t cb_pair(uint32_t sa, uint32_t sb) {
   if constexpr (CB == CB_MUL1) {
     // h = fp16 bits 0x6400 + bytesum(x) = 1024 + bytesum exactly; v = fma(h, 0x1EEE, 0xC931) rounded once
@@ -140,18 +150,19 @@ __device__ __forceinline__ uint32_t cb_pair(uint32_t sa, uint32_t sb) {
     const half2_t bias = __builtin_bit_cast(half2_t, 0xC931C931u);
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(h, inv, bias));
   } else {
-    return half_sums(cb_hash_masked<CB>(sa), cb_hash_masked<CB>(sb));
+    return half_sums<MFMA_NEXT>(cb_hash_masked<CB>(sa), cb_hash_masked<CB>(sb));
   }
 }
 
-// the lane's four decoded weights (rows 2j, 2j+1, 2j+8, 2j+9 of column c) as an MFMA operand
-template <int K, int CB>
+// the lane's four decoded weights (rows 2j, 2j+1, 2j+8, 2j+9 of column c) as an MFMA operand (MFMA_NEXT), or as
+// values to store
+template <int K, int CB, bool MFMA_NEXT = true>
 __device__ __forceinline__ half4_t decode_group(uint32_t w0, uint32_t w1, const LaneGeo& g) {
   uint32_t s[4];
   group_states<K>(w0, w1, g, s);
   uint2_t p;
-  p.x = cb_pair<CB>(s[0], s[1]);
-  p.y = cb_pair<CB>(s[2], s[3]);
+  p.x = cb_pair<CB, MFMA_NEXT>(s[0], s[1]);
+  p.y = cb_pair<CB, MFMA_NEXT>(s[2], s[3]);
   return __builtin_bit_cast(half4_t, p);
 }
 

@@ -328,7 +328,7 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
     uint8_t* dst = b_lds + (i & 1) * kBStage;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      const half4_t v = decode_group<K, CB>(bw[t][0], bw[t][1], g);
+      const half4_t v = decode_group<K, CB, false>(bw[t][0], bw[t][1], g);  // stored to LDS: no MFMA wait states
       *reinterpret_cast<half4_t*>(dst + (((btc + t) * 64 + l) * 16) + btr * 8) = v;
     }
   };
