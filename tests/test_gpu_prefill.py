@@ -130,7 +130,8 @@ def test_prefill_few_rows_many_contributors(coracle, M, n):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("rows,k,ns", [(37, 512, (256,)), (2200, 640, (512, 128, 256)), (8200, 2048, (128,))])
+@pytest.mark.parametrize("rows,k,ns", [(1, 128, (128,)), (5, 384, (256, 128)), (37, 512, (256,)), (333, 1280, (128, 128, 384, 256)),
+                                        (2200, 640, (512, 128, 256)), (8200, 2048, (128,))])
 def test_prefill_rotation_layouts_bit_identical(bf16, rows, k, ns):
     """The input rotation has two kernels: 16 lanes per 128-value unit with 16-byte loads (x and every suh 16-byte
     aligned) and 32 lanes with 8-byte loads (otherwise).  Both run the butterfly's stages in the same order on the
