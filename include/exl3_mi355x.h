@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 4
+#define EXL3_ABI_VERSION 5
 
 enum {
   EXL3_OK = 0,
@@ -81,10 +81,11 @@ int exl3_had_out_into(const void* y, int rows, int n, const void* svh, void* out
                       void* stream);
 
 /* ---- fused decode-GEMV / GEMM (subsystems 2, 3) --------------------------------------------------------------- */
-/* Workspace bytes exl3_linear / exl3_gemm_rotated need for `rows` rows of a group with input width k and
- * `n_total` output columns (n_total / 128 at most EXL3_WORKSPACE_COUNTER_BYTES / 4); 0 means none.  Deterministic in its
- * arguments.  The workspace holds the split counters (EXL3_WORKSPACE_COUNTER_BYTES, zero before the first use) and
- * fp32 split partials; calls that share a workspace must be ordered on one stream. */
+/* Workspace bytes exl3_linear needs for `rows` rows of a group with input width k and `n_total` output columns
+ * (n_total / 128 at most EXL3_WORKSPACE_COUNTER_BYTES / 4); 0 means none.  Deterministic in its arguments.  The
+ * workspace holds the split counters (EXL3_WORKSPACE_COUNTER_BYTES, zero before the first use) and fp32 split
+ * partials; calls that share a workspace must be ordered on one stream.  exl3_linear checks the workspace against the
+ * split plans of its own launches and returns EXL3_ERR_INVALID, launching nothing, when it is short. */
 size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K);
 
 /* y[rows, sum n_s] = concat_s( Had128(Had128(x * suh_s) @ W_s) * svh_s ) with fp32 accumulation; fp16 output of
@@ -95,9 +96,14 @@ size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K);
 int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards, int K,
                 int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes of exl3_gemm_rotated for `rows` rows (below 65 rows those of its decode-GEMV launches, from 65 rows
+ * those of the prefill decode-GEMM); 0 for bad shapes.  Same counter-region contract as exl3_linear_workspace_bytes. */
+size_t exl3_gemm_rotated_workspace_bytes(int rows, int k, int n, int K);
 /* out fp16 [rows, n] = xh @ W_inner in the rotated basis (no Hadamards, no sign vectors); fp32 accumulation, one
- * rounding to fp16.  Identity rows of xh read W_inner out exactly.  Replaces exl3_gemm_marlin
- * (cuda/csrc/exl3_marlin.cu:411-423), the one-hot test entry of cuda/src/sglang_exl3/parity/marlin_parity.py:149-159. */
+ * rounding to fp16; xh fp16 [rows, k].  Identity rows of xh read W_inner out exactly.  The rows run through the kernel
+ * that serves the same row count in a linear: below 65 rows the decode-GEMV (one 16-row group per launch, two decoded
+ * tiles per MFMA), from 65 rows the prefill decode-GEMM.  Replaces exl3_gemm_marlin (cuda/csrc/exl3_marlin.cu:411-423),
+ * the one-hot test entry of cuda/src/sglang_exl3/parity/marlin_parity.py:149-159. */
 int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook, void* out,
                       void* workspace, size_t workspace_bytes, void* stream);
 
@@ -106,7 +112,8 @@ int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int 
  * hipMalloc).  Same arguments as exl3_linear without the workspace, and the same results up to 16 rows (past 16 rows
  * it runs one launch per 16 rows, where exl3_linear shares each decoded tile among up to 64 rows: the two then agree
  * to rounding): the split counters and fp32 partials live in a scratch array of EXL3_NOALLOC_SCRATCH_BYTES that the
- * library holds on every GPU it runs on until the process ends.  It calls no allocating routine.  A call whose
+ * library holds on every GPU it runs on until the process ends, on the GPU of `stream` (the current device for the
+ * null stream).  It calls no allocating routine.  A call whose
  * workspace need (that of 16-row launches; exl3_linear_workspace_bytes up to 16 rows) exceeds the scratch returns
  * EXL3_ERR_INVALID and launches nothing.  All calls on one GPU share its scratch: calls that overlap
  * in time on one GPU (several streams, several host threads without ordering) race and give wrong results; calls

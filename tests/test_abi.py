@@ -3,6 +3,7 @@ arguments before any device work (the reference's TORCH_CHECK paths, cuda/csrc/e
 import ctypes
 
 import pytest
+import torch
 
 from trellis_serve_amd import _lib
 
@@ -22,7 +23,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.exl3_abi_version() == 4
+    assert lib.exl3_abi_version() == 5
 
 
 def test_workspace_size_is_deterministic_and_zero_for_bad_shapes(lib):
@@ -84,3 +85,41 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
 
 def test_shard_struct_layout():
     assert ctypes.sizeof(_lib.Exl3Shard) == 32
+
+
+def test_noalloc_rejects_calls_beyond_the_scratch(lib):
+    """A call whose workspace would exceed the scratch is refused before any launch (no device pointer is used)."""
+    k, n, rows = 8192, 131072, 16
+    assert lib.exl3_linear_workspace_bytes(rows, k, n, 3) > lib.exl3_linear_noalloc_max_bytes()
+    arr = (_lib.Exl3Shard * 1)(_lib.Exl3Shard(1, 1, 1, n))
+    assert lib.exl3_linear_noalloc(1, 0, rows, k, arr, 1, 3, 1, 1, 0, None) == _lib.EXL3_ERR_INVALID
+    assert "scratch" in lib.exl3_last_error().decode()
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="passes placeholder pointers: only where no GPU can run them")
+def test_reported_workspace_sizes_cover_every_launch_plan(lib):
+    """Each entry point checks its workspace against the split plans of exactly the launches it is about to make,
+    before any HIP call.  With no GPU present a call that passes that check fails at its first launch (EXL3_ERR_HIP),
+    one that does not returns EXL3_ERR_INVALID: so over a grid of shapes and every row count up to 64 (and a few
+    prefill row counts) the size each size function reports must get past the check, and 256 bytes less must not."""
+    P = 0x1000   # placeholder device pointer: never dereferenced on this path
+    ks = (128, 1280, 4096, 11008, 17408)
+    ns = (128, 1024, 5120, 17408, 34816)
+    for K in (2, 3, 8):
+        for k in ks:
+            for n in ns:
+                for rows in list(range(1, 65)) + [65, 130, 600]:
+                    need = lib.exl3_gemm_rotated_workspace_bytes(rows, k, n, K)
+                    assert need > 0
+                    assert lib.exl3_gemm_rotated(P, rows, k, P, n, K, 0, P, P, need, None) == _lib.EXL3_ERR_HIP, \
+                        (K, k, n, rows, lib.exl3_last_error())
+                    assert lib.exl3_gemm_rotated(P, rows, k, P, n, K, 0, P, P, need - 256, None) == \
+                        _lib.EXL3_ERR_INVALID, (K, k, n, rows)
+                    if rows > 64:
+                        continue
+                    arr = (_lib.Exl3Shard * 1)(_lib.Exl3Shard(P, P, P, n))
+                    need = lib.exl3_linear_workspace_bytes(rows, k, n, K)
+                    assert lib.exl3_linear(P, 0, rows, k, arr, 1, K, 1, P, 0, P, need, None) == _lib.EXL3_ERR_HIP, \
+                        (K, k, n, rows, lib.exl3_last_error())
+                    assert lib.exl3_linear(P, 0, rows, k, arr, 1, K, 1, P, 0, P, need - 256, None) == \
+                        _lib.EXL3_ERR_INVALID, (K, k, n, rows)

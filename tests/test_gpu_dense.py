@@ -86,12 +86,116 @@ def test_reconstruct_covers_every_state(cb):
 @pytest.mark.parametrize("K", KS)
 @pytest.mark.parametrize("cb", CBS)
 def test_gemm_rotated_one_hot_readout_is_exact(coracle, K, cb):
+    """256 identity rows go through the prefill decode-GEMM (65 rows and more), 64 at a time through the decode-GEMV
+    (16-row launches, two decoded tiles per MFMA): both read W_inner back bit for bit."""
     rng = np.random.default_rng(2000 + 10 * K + cb)
     k, n = 256, 256
     tr = _trellis(rng, k, n, K)
+    dtr = _dev(tr)
+    ref = c_reconstruct(coracle, tr, K, cb).view(np.uint16)
     xh = torch.eye(k, dtype=torch.float16, device="cuda")
-    w = _ops().gemm_rotated(xh, _dev(tr), cb).cpu().numpy()
-    np.testing.assert_array_equal(w.view(np.uint16), c_reconstruct(coracle, tr, K, cb).view(np.uint16))
+    w = _ops().gemm_rotated(xh, dtr, cb).cpu().numpy()
+    np.testing.assert_array_equal(w.view(np.uint16), ref)
+    w = torch.cat([_ops().gemm_rotated(xh[r0:r0 + 64].contiguous(), dtr, cb) for r0 in range(0, k, 64)])
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint16), ref)
+
+
+def _halves_sum_lut(cb):
+    """lo + hi of every state's masked hash, unrounded (float64): the weight a kernel would use if it added the two
+    fp16 halves in the matrix core instead of rounding their sum to fp16 first (codebook.cuh:56-75 rounds, __hadd)."""
+    s = np.arange(65536, dtype=np.uint64)
+    x = (s * orc.MCG_MULT) if cb == 1 else (s * orc.INST3_MULT + orc.INST3_ADD)
+    x = ((x & 0xFFFFFFFF) & 0x8FFF8FFF) ^ 0x3B603B60
+    lo = (x & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (x >> 16).astype(np.uint16).view(np.float16).astype(np.float64)
+    return lo + hi
+
+
+@pytest.mark.parametrize("cb", (0, 1))
+@pytest.mark.parametrize("K", (2, 3, 4))
+def test_gemv_multiplies_by_rounded_weights(K, cb):
+    """Rows x = e_i + e_j give fp16(w_i + w_j) per column.  With trellis_core's rounded weights w = fp16(lo + hi)
+    (reference.py:52-73) the sum of the two products is exact in fp32 and rounds once; a kernel that fed the matrix
+    core the unsummed halves would return fp16((lo_i + hi_i) + (lo_j + hi_j)) instead.  The pairs are chosen where the
+    two differ, so this fails for the unsummed form; checked through the decode-GEMV (16 rows) and the decode-GEMM
+    (80 rows).  Columns where a weight is below 2^-10 (its fp32 sum with the other could round) are left out."""
+    rng = np.random.default_rng(2700 + 10 * K + cb)
+    k, n = 512, 256
+    tr = _trellis(rng, k, n, K)
+    states = orc.decode_states(tr.reshape(-1, 16 * K), K)            # [tiles, 256] stream order
+    perm = orc.tensor_core_perm()
+    w_rnd = orc.codebook_lut(cb).astype(np.float64)[states]
+    w_sum = _halves_sum_lut(cb)[states]
+
+    def inner(v):   # stream order -> [k, n] as reconstruct_inner places it
+        t = np.empty_like(v)
+        t[:, perm] = v
+        return t.reshape(k // 16, n // 16, 16, 16).transpose(0, 2, 1, 3).reshape(k, n)
+
+    W, E = inner(w_rnd), inner(w_sum)
+    pairs = []
+    for c in range(n):
+        if len(pairs) == 80:
+            break
+        good = np.abs(W[:, c]) >= 2.0 ** -10
+        for i in rng.permutation(np.flatnonzero(good))[:64]:
+            js = np.flatnonzero(good & (np.arange(k) != i))
+            want = (W[i, c] + W[js, c]).astype(np.float16)
+            halves = (E[i, c] + E[js, c]).astype(np.float16)
+            bad = js[want != halves]
+            if bad.size:
+                pairs.append((i, bad[0]))
+                break
+    assert len(pairs) == 80, len(pairs)
+    x = np.zeros((80, k), dtype=np.float16)
+    for r, (i, j) in enumerate(pairs):
+        x[r, i] = x[r, j] = 1
+    ii, jj = np.array(pairs).T
+    want = (W[ii] + W[jj]).astype(np.float16)
+    halves = (E[ii] + E[jj]).astype(np.float16)
+    keep = (np.abs(W[ii]) >= 2.0 ** -10) & (np.abs(W[jj]) >= 2.0 ** -10)
+    dtr = _dev(tr)
+    for rows in (16, 80):
+        got = torch.cat([_ops().gemm_rotated(_dev(x[r0:r0 + rows]), dtr, cb) for r0 in range(0, 80, rows)])
+        got = got.cpu().numpy()
+        assert np.array_equal(got.view(np.uint16)[keep], want.view(np.uint16)[keep]), rows
+        assert (got != halves).any(axis=1).all(), rows   # every row differs from the unsummed-halves result
+
+
+def test_gemm_rotated_17_to_31_rows_in_its_reported_workspace(coracle):
+    """gemm_rotated serves 17-31 rows as 16-row GEMV launches; their split plan (one row group) takes more fp32
+    partials than exl3_linear's plan of the same row count, so the workspace is sized and checked for its own launches
+    (the shape once overflowed: k = 11008, n = 5120, K = 2, 3INST).  One-hot rows read W_inner back exactly."""
+    ops = _ops()
+    ops.release_workspaces()
+    rng = np.random.default_rng(2800)
+    k, n, K, cb = 11008, 5120, 2, 0
+    tr = _trellis(rng, k, n, K)
+    dtr = _dev(tr)
+    ref = c_reconstruct(coracle, tr, K, cb).view(np.uint16)
+    eye = torch.eye(k, dtype=torch.float16, device="cuda")
+    for rows, r0 in ((17, 0), (23, 4000), (31, k - 31)):
+        got = ops.gemm_rotated(eye[r0:r0 + rows].contiguous(), dtr, cb).cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint16), ref[r0:r0 + rows], err_msg=str(rows))
+
+
+def test_row_counts_either_side_of_the_row_group_switch_agree(coracle):
+    """16 rows run one row group (two tiles per 16x16x32 MFMA), 17 rows two groups (16x16x16 MFMAs per tile): both
+    multiply by the same rounded weights, so a row's output differs only by fp32 summation order -- well inside the
+    layer tolerance, and both meet the oracle."""
+    rng = np.random.default_rng(2900)
+    k, n, K, cb = 4096, 2048, 3, 1
+    tr, suh, svh = _trellis(rng, k, n, K), _signs(rng, k), _signs(rng, n)
+    args = ([_dev(tr)], [_dev(suh)], [_dev(svh)], cb)
+    x = rng.standard_normal((17, k)).astype(np.float16)
+    y17 = _ops().linear(_dev(x), *args).cpu().numpy().astype(np.float64)
+    y16 = _ops().linear(_dev(x[:16]), *args).cpu().numpy().astype(np.float64)
+    d = np.linalg.norm(y17[:16] - y16) / np.linalg.norm(y16)
+    assert d <= 2e-4, d
+    ref = orc.linear_forward(x, tr, suh, svh, K, cb, w_inner=c_reconstruct(coracle, tr, K, cb), dtype=np.float64)
+    for y, r in ((y16, ref[:16]), (y17, ref)):
+        nrel, mrel = _errs(y, r)
+        assert nrel <= TOL and mrel <= TOL, (nrel, mrel)
 
 
 @pytest.mark.parametrize("K", KS)
@@ -117,7 +221,7 @@ def test_repack_is_lossless_and_the_kernels_read_it(coracle, K):
 def test_one_hot_readout_through_the_split_k_gemv_is_exact(coracle, K, cb):
     """The decode-GEMV (split-K: every k split of a 128-column block writes fp32 partials, the last arrival sums
     them) read back with one-hot rows: each row of W_inner comes back bit for bit, 4 rows per call and once with a
-    single row (the two-halves MFMA path below 8 rows).  1280 x 16384 has 10 k blocks and 128 column blocks."""
+    single row.  1280 x 16384 has 10 k blocks and 128 column blocks."""
     rng = np.random.default_rng(2500 + 10 * K + cb)
     k, n = 1280, 16384
     tr = _trellis(rng, k, n, K)

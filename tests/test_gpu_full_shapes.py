@@ -61,7 +61,7 @@ def test_gemv_c2_layer_set_shapes(name, M):
 
 
 @pytest.mark.parametrize("K,cb,M", [(3, 1, 2048), (2, 0, 512), (8, 2, 512), (3, 1, 8192), (4, 2, 2048), (5, 1, 2048),
-                                    (6, 0, 2048)])
+                                    (6, 0, 2048), (2, 0, 2048), (8, 2, 2048)])
 def test_prefill_c3_shape(K, cb, M):
     """the 5120 -> 17408 prefill decode-GEMM (68 column tiles, split-K tail items) at the benchmark's K,
     codebook and row counts."""
@@ -102,3 +102,24 @@ def test_full_shape_column_slices_against_the_oracle(coracle, name, M, K, cb, fn
             mrel = np.abs(got - ref).max() / np.abs(ref).max()
             assert nrel <= TOL and mrel <= TOL, (cbk, nrel, mrel)
         col += tn * 16
+
+
+@pytest.mark.parametrize("K", (2, 3, 4, 5, 6, 8))
+@pytest.mark.parametrize("cb", (0, 1, 2))
+def test_prefill_gemm_one_hot_readout_on_c3_column_slices(coracle, K, cb):
+    """The decoded weights of the prefill decode-GEMM read back bit for bit (the method of
+    cuda/src/sglang_exl3/parity/marlin_parity.py:149-159): 5120 identity rows through exl3_gemm_rotated take the
+    decode-GEMM (no rotations), on two column slices of a C3 (5120 -> 17408) trellis -- 768 columns from the start
+    (three 256-column tiles) and 640 from the end (the last a half tile) -- against the C restatement's decode.  With
+    20 row blocks the launch shares tiles out by k-step runs, so partial tiles are summed too (zeros but one term)."""
+    import numpy as np
+    from conftest import c_reconstruct
+    rng = np.random.default_rng(400 + 10 * K + cb)
+    k, n = 5120, 17408
+    tr = rng.integers(-32768, 32768, size=(k // 16, n // 16, 16 * K), dtype=np.int16)
+    eye = torch.eye(k, dtype=torch.float16, device="cuda")
+    for c0, c1 in ((0, 768), (n - 640, n)):
+        sl = np.ascontiguousarray(tr[:, c0 // 16:c1 // 16])
+        got = _ops().gemm_rotated(eye, torch.from_numpy(sl).cuda(), cb).cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint16), c_reconstruct(coracle, sl, K, cb).view(np.uint16),
+                                      err_msg=f"columns {c0}:{c1}")

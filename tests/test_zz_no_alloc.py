@@ -71,13 +71,3 @@ def test_noalloc_equals_workspace_entry_on_two_calls(K, cb):
             got = y0[:, col:col + n].cpu().numpy().astype(np.float64)
             assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2e-3
             col += n
-
-
-def test_noalloc_rejects_calls_beyond_the_scratch():
-    """A call whose workspace would exceed the scratch is refused before any launch."""
-    lib = _lib().load()
-    k, n, rows = 8192, 131072, 16
-    assert lib.exl3_linear_workspace_bytes(rows, k, n, 3) > lib.exl3_linear_noalloc_max_bytes()
-    arr = (_lib().Exl3Shard * 1)(_lib().Exl3Shard(1, 1, 1, n))
-    assert lib.exl3_linear_noalloc(1, 0, rows, k, arr, 1, 3, 1, 1, 0, None) == _lib().EXL3_ERR_INVALID
-    assert "scratch" in lib.exl3_last_error().decode()

@@ -52,6 +52,7 @@ _SIGNATURES: dict[str, tuple] = {
     "exl3_had_out_into": (_I, [_P, _I, _I, _P, _P, _I, _I, _I, _P]),
     "exl3_linear_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "exl3_linear": (_I, [_P, _I, _I, _I, ctypes.POINTER(Exl3Shard), _I, _I, _I, _P, _I, _P, _SZ, _P]),
+    "exl3_gemm_rotated_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "exl3_gemm_rotated": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _P, _SZ, _P]),
     "exl3_linear_noalloc_max_bytes": (_SZ, []),
     "exl3_linear_noalloc": (_I, [_P, _I, _I, _I, ctypes.POINTER(Exl3Shard), _I, _I, _I, _P, _I, _P]),

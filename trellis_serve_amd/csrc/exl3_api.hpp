@@ -32,6 +32,16 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 constexpr size_t kCounterBytes = EXL3_WORKSPACE_COUNTER_BYTES;
 constexpr int kMaxCounters = (int)(kCounterBytes / sizeof(int));
 
+// Rows from which a linear's rows go to the prefill decode-GEMM instead of the decode-GEMV (the dispatch of the
+// torch-facing op, measured crossover on the 27B shapes); exl3_gemm_rotated switches at the same count.
+constexpr int kPrefillRows = 65;
+
+// The rotation-free prefill decode-GEMM of exl3_gemm_rotated (out = xh @ W_inner, fp16 xh), defined with the prefill
+// kernels: its workspace bytes, and the call.
+size_t prefill_plain_workspace_bytes(int rows, int k, int n);
+int prefill_plain_gemm(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook, void* out,
+                       void* workspace, size_t workspace_bytes, hipStream_t st);
+
 inline bool valid_bits(int K) { return K == 2 || K == 3 || K == 4 || K == 5 || K == 6 || K == 8; }
 inline bool valid_cb(int cb) { return cb >= 0 && cb <= 2; }
 

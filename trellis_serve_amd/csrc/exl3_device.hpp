@@ -166,23 +166,38 @@ __device__ __forceinline__ half4_t decode_group(uint32_t w0, uint32_t w1, const 
   return __builtin_bit_cast(half4_t, p);
 }
 
-// The lane's four weights as their unsummed fp16 halves, for the GEMV: dword e of the result is the masked hash of
-// state e, i.e. the pair [lo_e, hi_e] whose fp16 sum is weight e (MCG / 3INST only).  As the 8-half B operand of
-// v_mfma_f32_16x16x32_f16 against activations staged twice ([a0, a0, a1, a1, ...]) the matrix core forms
-// a*lo + a*hi in fp32, where the exact layer has a * fp16(lo + hi): the mask keeps both halves' exponent fields in
-// 12..15 (magnitudes in [1/8, 2)), so lo + hi is exact in fp32 and differs from the rounded weight by at most half
-// an fp16 ulp of it, inside the layer tolerance.  A one-hot activation row reads fp16(lo + hi) back exactly: the
-// sum of two exact products, rounded once to fp16, is the rounded weight (__hadd rounds the same exact sum).  This
-// drops the per-weight fp16 add, a quarter of the decode's VALU work.
+// The lane's weights of two tiles (its group of tile a, then of tile b) as one 8-half MFMA 16x16x32 B fragment,
+// rounded as decode_group rounds them.  For MCG / 3INST the eight half sums sit in one asm block, so one set of MFMA
+// wait states follows all of them (the compiler may order separate blocks either way round).
 template <int K, int CB>
-__device__ __forceinline__ half8_t decode_group_halves(uint32_t w0, uint32_t w1, const LaneGeo& g) {
-  static_assert(CB != CB_MUL1, "MUL1 has no two-halves form: its weight is one rounded FMA");
-  uint32_t s[4];
-  group_states<K>(w0, w1, g, s);
+__device__ __forceinline__ half8_t decode_two_groups(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
+                                                     const LaneGeo& g) {
+  uint32_t s[8];
+  group_states<K>(a0, a1, g, s);
+  group_states<K>(b0, b1, g, s + 4);
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = {cb_hash_masked<CB>(s[0]), cb_hash_masked<CB>(s[1]), cb_hash_masked<CB>(s[2]),
-                   cb_hash_masked<CB>(s[3])};
-  return __builtin_bit_cast(half8_t, v);
+  u32x4 r;
+  if constexpr (CB == CB_MUL1) {
+    r = u32x4{cb_pair<CB>(s[0], s[1]), cb_pair<CB>(s[2], s[3]), cb_pair<CB>(s[4], s[5]), cb_pair<CB>(s[6], s[7])};
+  } else {
+    uint32_t y[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) y[e] = cb_hash_masked<CB>(s[e]);
+    uint32_t r0, r1, r2, r3;
+    asm("v_add_f16_sdwa %0, %4, %4 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %1, %6, %6 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %2, %8, %8 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %3, %10, %10 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %0, %5, %5 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %1, %7, %7 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %2, %9, %9 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "v_add_f16_sdwa %3, %11, %11 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+        "s_nop 2"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+        : "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]), "v"(y[4]), "v"(y[5]), "v"(y[6]), "v"(y[7]));
+    r = u32x4{r0, r1, r2, r3};
+  }
+  return __builtin_bit_cast(half8_t, r);
 }
 
 // ---- fp16 / bf16 boundary conversions (torch value conversions, RNE) -----------------------------------------

@@ -48,6 +48,7 @@ namespace exl3 {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 256, kBN = 256, kBK = 32;
 constexpr int kGemmWaves = 8, kGemmThreads = kGemmWaves * 64;
@@ -107,6 +108,46 @@ __device__ __forceinline__ const uint16_t* unit_suh(const ShardSuh& su_all, int 
   return s == 0 ? su_all.suh[0] : s == 1 ? su_all.suh[1] : s == 2 ? su_all.suh[2] : su_all.suh[3];
 }
 
+// The 8 values of a 16-lane unit's lane (positions 8t .. 8t+7) as 4 fp16 pairs: fp16(Had(fp16(x) * suh)) (ROT), or
+// x as given (fp16 rows)
+template <bool X_BF16, bool ROT>
+__device__ __forceinline__ void frag16_values(u32x4_t xv, u32x4_t sv, uint32_t d[4]) {
+  if constexpr (!ROT) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) d[q] = xv[q];
+    return;
+  }
+  const half8_t sc = __builtin_bit_cast(half8_t, sv);
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t w = xv[i >> 1];
+    const uint16_t raw = (uint16_t)((i & 1) ? w >> 16 : w & 0xFFFF);
+    const _Float16 v = X_BF16 ? (_Float16)bf16_to_f32(raw) : __builtin_bit_cast(_Float16, raw);
+    f[i] = (float)(_Float16)(v * sc[i]);
+  }
+#pragma unroll
+  for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (!(i & h)) {
+        const float a = f[i], bb = f[i + h];
+        f[i] = a + bb;
+        f[i + h] = a - bb;
+      }
+  had_stage<1>(f[0], f[1], f[2], f[3]);
+  had_stage<1>(f[4], f[5], f[6], f[7]);
+  had_stage<2>(f[0], f[1], f[2], f[3]);
+  had_stage<2>(f[4], f[5], f[6], f[7]);
+  had_stage<4>(f[0], f[1], f[2], f[3]);
+  had_stage<4>(f[4], f[5], f[6], f[7]);
+  had_stage<8>(f[0], f[1], f[2], f[3]);
+  had_stage<8>(f[4], f[5], f[6], f[7]);
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    d[q] = __builtin_bit_cast(uint32_t, half2_t{had_scale_f16(f[2 * q]), had_scale_f16(f[2 * q + 1])});
+}
+
 // The same rotation with 16 lanes per 128-value (row, block) unit: lane t holds positions 8t .. 8t+7, read with one
 // 16-byte load of x and one of suh (x and every suh 16-byte aligned; the host checks).  The butterfly runs the stages
 // of had128_x4 in the same order on the same pairs -- h = 1, 2, 4 inside the lane (h = 4 was the lane-xor-1 stage
@@ -114,10 +155,11 @@ __device__ __forceinline__ const uint16_t* unit_suh(const ShardSuh& su_all, int 
 // so the rotated values are bit-identical.  Fragment order: lane t (a = t & 3) holds, per q = 0..3, the slot pair
 // (q, tr = a >> 1, e = 2 (a & 1) + 0/1); lanes a and a ^ 1 swap two dwords (DPP) so that each stores two 8-byte
 // slot groups (q, tr) whole.  A 16-lane group takes U consecutive units with all loads issued first.
-template <bool X_BF16, int U>
+// ROT = false: the fp16 rows are taken as given (no sign vector, no butterfly, no rounding) and only put in fragment
+// order (the rotation-free GEMM of exl3_gemm_rotated).
+template <bool X_BF16, int U, bool ROT = true>
 __global__ __launch_bounds__(256) void had_in_frag16_kernel(const void* __restrict__ x, int rows, int k,
                                                             ShardSuh su_all, int shards, uint16_t* __restrict__ xh) {
-  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
   const int kb = k >> 7;
   const int units = shards * rows * kb;
   const int u0 = (blockIdx.x * 16 + (threadIdx.x >> 4)) * U;
@@ -130,43 +172,15 @@ __global__ __launch_bounds__(256) void had_in_frag16_kernel(const void* __restri
     const int s = u / (rows * kb), rem = u - s * rows * kb, r = rem / kb, b = rem - r * kb;
     const int kk = b * 128 + 8 * t;
     xv[j] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(x) + (size_t)r * k + kk);
-    sv[j] = *reinterpret_cast<const u32x4_t*>(unit_suh(su_all, s) + kk);
+    sv[j] = ROT ? *reinterpret_cast<const u32x4_t*>(unit_suh(su_all, s) + kk) : u32x4_t{0u, 0u, 0u, 0u};
   }
 #pragma unroll
   for (int j = 0; j < U; j++) {
     const int u = u0 + j;
     if (u >= units) break;
     const int s = u / (rows * kb), rem = u - s * rows * kb, r = rem / kb, b = rem - r * kb;
-    const half8_t sc = __builtin_bit_cast(half8_t, sv[j]);
-    float f[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t w = xv[j][i >> 1];
-      const uint16_t raw = (uint16_t)((i & 1) ? w >> 16 : w & 0xFFFF);
-      const _Float16 v = X_BF16 ? (_Float16)bf16_to_f32(raw) : __builtin_bit_cast(_Float16, raw);
-      f[i] = (float)(_Float16)(v * sc[i]);
-    }
-#pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-      for (int i = 0; i < 8; i++)
-        if (!(i & h)) {
-          const float a = f[i], bb = f[i + h];
-          f[i] = a + bb;
-          f[i + h] = a - bb;
-        }
-    had_stage<1>(f[0], f[1], f[2], f[3]);
-    had_stage<1>(f[4], f[5], f[6], f[7]);
-    had_stage<2>(f[0], f[1], f[2], f[3]);
-    had_stage<2>(f[4], f[5], f[6], f[7]);
-    had_stage<4>(f[0], f[1], f[2], f[3]);
-    had_stage<4>(f[4], f[5], f[6], f[7]);
-    had_stage<8>(f[0], f[1], f[2], f[3]);
-    had_stage<8>(f[4], f[5], f[6], f[7]);
     uint32_t d[4];  // d[q] = fp16 pair (positions 2q, 2q+1 of the lane)
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-      d[q] = __builtin_bit_cast(uint32_t, half2_t{had_scale_f16(f[2 * q]), had_scale_f16(f[2 * q + 1])});
+    frag16_values<X_BF16, ROT>(xv[j], sv[j], d);
     const bool low = (t & 1) == 0;
     // lane a (even) stores q = 0, 2 as [own, partner's]; lane a + 1 stores q = 1, 3 as [partner's, own]
     const uint32_t g0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)(low ? d[1] : d[0]), 0xB1, 0xF, 0xF, false);
@@ -180,11 +194,38 @@ __global__ __launch_bounds__(256) void had_in_frag16_kernel(const void* __restri
   }
 }
 
+// The 4 values of a 32-lane unit's lane (positions 4t .. 4t+3) as 2 fp16 pairs: fp16(Had(fp16(x) * suh)) (ROT), or
+// x as given (fp16 rows)
+template <bool X_BF16, bool ROT>
+__device__ __forceinline__ void frag_values(uint2_t xv, uint2_t sv, uint32_t& lo_w, uint32_t& hi_w) {
+  if constexpr (!ROT) {
+    lo_w = xv.x;
+    hi_w = xv.y;
+    return;
+  }
+  _Float16 v[4];
+  if constexpr (X_BF16) {
+    v[0] = (_Float16)bf16_to_f32((uint16_t)(xv.x & 0xFFFF));
+    v[1] = (_Float16)bf16_to_f32((uint16_t)(xv.x >> 16));
+    v[2] = (_Float16)bf16_to_f32((uint16_t)(xv.y & 0xFFFF));
+    v[3] = (_Float16)bf16_to_f32((uint16_t)(xv.y >> 16));
+  } else {
+    const half4_t raw = __builtin_bit_cast(half4_t, xv);
+    v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+  }
+  const half4_t sc = __builtin_bit_cast(half4_t, sv);
+  float f0 = (float)(_Float16)(v[0] * sc.x), f1 = (float)(_Float16)(v[1] * sc.y);
+  float f2 = (float)(_Float16)(v[2] * sc.z), f3 = (float)(_Float16)(v[3] * sc.w);
+  had128_x4(f0, f1, f2, f3);
+  lo_w = __builtin_bit_cast(uint32_t, half2_t{had_scale_f16(f0), had_scale_f16(f1)});
+  hi_w = __builtin_bit_cast(uint32_t, half2_t{had_scale_f16(f2), had_scale_f16(f3)});
+}
+
 // rotated activations in fragment order: xh_f[s*rows + r][k] for shard s (see the header comment).  A half-wave
 // takes U consecutive 128-value (row, block) units, issues all their loads first (one round of load latency per
 // half-wave instead of one per unit), then rotates and stores each; lane t holds positions 4t .. 4t+3 of a block.
 // U = 4 from 2^17 units (measured at 8192 rows: 60 -> 52 us; equal at 2048 rows, slower at 512 rows).
-template <bool X_BF16, int U>
+template <bool X_BF16, int U, bool ROT = true>
 __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict__ x, int rows, int k, ShardSuh su_all,
                                                           int shards, uint16_t* __restrict__ xh) {
   const int kb = k >> 7;
@@ -198,30 +239,16 @@ __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict
     const int u = min(u0 + j, units - 1);  // past the end: a repeat of the last unit, not stored
     const int s = u / (rows * kb), rem = u - s * rows * kb, r = rem / kb, b = rem - r * kb;
     const int kk = b * 128 + 4 * t;
-    const uint16_t* su = unit_suh(su_all, s);
     xv[j] = *reinterpret_cast<const uint2_t*>(static_cast<const uint16_t*>(x) + (size_t)r * k + kk);
-    sv[j] = *reinterpret_cast<const uint2_t*>(su + kk);
+    sv[j] = ROT ? *reinterpret_cast<const uint2_t*>(unit_suh(su_all, s) + kk) : uint2_t{0u, 0u};
   }
 #pragma unroll
   for (int j = 0; j < U; j++) {
     const int u = u0 + j;
     if (u >= units) break;
     const int s = u / (rows * kb), rem = u - s * rows * kb, r = rem / kb, b = rem - r * kb;
-    _Float16 v[4];
-    if constexpr (X_BF16) {
-      v[0] = (_Float16)bf16_to_f32((uint16_t)(xv[j].x & 0xFFFF));
-      v[1] = (_Float16)bf16_to_f32((uint16_t)(xv[j].x >> 16));
-      v[2] = (_Float16)bf16_to_f32((uint16_t)(xv[j].y & 0xFFFF));
-      v[3] = (_Float16)bf16_to_f32((uint16_t)(xv[j].y >> 16));
-    } else {
-      const half4_t raw = __builtin_bit_cast(half4_t, xv[j]);
-      v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
-    }
-    const half4_t sc = __builtin_bit_cast(half4_t, sv[j]);
-    float f0 = (float)(_Float16)(v[0] * sc.x), f1 = (float)(_Float16)(v[1] * sc.y);
-    float f2 = (float)(_Float16)(v[2] * sc.z), f3 = (float)(_Float16)(v[3] * sc.w);
-    had128_x4(f0, f1, f2, f3);
-    const half2_t lo = {had_scale_f16(f0), had_scale_f16(f1)}, hi = {had_scale_f16(f2), had_scale_f16(f3)};
+    uint32_t lo_w, hi_w;  // fp16 pairs: positions 4t, 4t+1 and 4t+2, 4t+3
+    frag_values<X_BF16, ROT>(xv[j], sv[j], lo_w, hi_w);
     // k-step major: the 32 halves of row r in k-step kt (one MFMA k-block) at [kt][r][32], so that one k-step of a
     // row block is one contiguous run and every 16-row A piece of the GEMM reads whole cache lines.  Inside a
     // 32-block, slot (q, tr, e) holds position 16 tr + 2q + (e & 1) + 8 (e >> 1).  With a = t & 3, lane t's positions
@@ -229,7 +256,6 @@ __global__ __launch_bounds__(256) void had_in_frag_kernel(const void* __restrict
     // e = 2, 3 of the same q.  The pair (a, a + 2) swaps one dword (a DPP quad permute) and each lane stores its q's
     // 4 slots as one 8-byte word.
     const bool low = (t & 2) == 0;
-    const uint32_t lo_w = __builtin_bit_cast(uint32_t, lo), hi_w = __builtin_bit_cast(uint32_t, hi);
     const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)(low ? hi_w : lo_w), 0x4E, 0xF, 0xF, false);
     const uint2_t out = low ? uint2_t{lo_w, got} : uint2_t{got, hi_w};
     const int blk32 = t >> 3, tr = (t >> 2) & 1, q = 2 * (t & 1) + (low ? 0 : 1);
@@ -625,65 +651,44 @@ extern "C" size_t exl3_prefill_workspace_bytes(int rows, int k, int n_total, int
   return need;
 }
 
-extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host,
-                                   int nshards, int K, int codebook, void* y, int y_bf16, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-  EXL3_CHECK_ARG(x && y && shards_host, "exl3_linear_prefill: null pointer");
-  EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_linear_prefill: K = %d / codebook = %d", K, codebook);
-  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_linear_prefill: rows = %d, k = %d", rows, k);
-  EXL3_CHECK_ARG(nshards >= 1 && nshards <= EXL3_MAX_SHARDS, "exl3_linear_prefill: nshards = %d", nshards);
-  if (rows == 0) return EXL3_OK;
-  EXL3_CHECK_ARG((int64_t)rows * k * 2 <= INT32_MAX, "exl3_linear_prefill: rows * k too large for one launch");
-  GemmShards sa{};
-  int col = 0, ctl = 0;
-  int shard_n[EXL3_MAX_SHARDS];
-  for (int s = 0; s < nshards; s++) {
-    const exl3_shard& sh = shards_host[s];
-    EXL3_CHECK_ARG(sh.trellis && sh.suh && sh.svh, "shard %d: null tensor pointer", s);
-    EXL3_CHECK_ARG(sh.n > 0 && sh.n % 128 == 0, "shard %d: n = %d is not a positive multiple of 128", s, sh.n);
-    EXL3_CHECK_ARG((int64_t)k * sh.n * K / 8 <= INT32_MAX, "shard %d: trellis exceeds the 2 GiB buffer range", s);
-    sa.trellis[s] = static_cast<const uint32_t*>(sh.trellis);
-    sa.svh[s] = static_cast<const uint16_t*>(sh.svh);
-    sa.xh[s] = reinterpret_cast<const uint16_t*>(static_cast<const uint8_t*>(workspace) + kCounterBytes) +
-               (size_t)s * rows * k;
-    sa.tn[s] = sh.n / 16;
-    sa.col0[s] = col;
-    sa.ct0[s] = ctl;
-    shard_n[s] = sh.n;
-    col += sh.n;
-    ctl += (sh.n / 128 + 1) / 2;
-  }
-  sa.ct0[nshards] = ctl;
-  sa.count = nshards;
+namespace exl3 {
+
+// The input pass (rotation of every shard in fragment order, or with ROT = false the rows as given in fragment order)
+// and the decode-GEMM launch of one call; sa holds the shards, its xh pointers into the workspace.
+template <bool ROT>
+static int launch_prefill(const void* x, bool x_bf16, int rows, int k, GemmShards& sa, const ShardSuh& su,
+                          const int* shard_n, int K, int codebook, void* y, bool y_bf16, void* workspace,
+                          size_t workspace_bytes, hipStream_t st, const char* what) {
+  const int nshards = sa.count;
   const GemmLayout L = gemm_layout(rows, k, gemm_col_tiles(shard_n, nshards), nshards);
-  EXL3_CHECK_ARG(workspace && workspace_bytes >= L.total, "exl3_linear_prefill: workspace %zu bytes, need %zu",
+  EXL3_CHECK_ARG(workspace && workspace_bytes >= L.total, "%s: workspace %zu bytes, need %zu", what,
                  workspace_bytes, L.total);
-  EXL3_CHECK_ARG(L.sk_tiles <= kMaxCounters, "exl3_linear_prefill: %d stream-K tiles exceed the counter region",
-                 L.sk_tiles);
+  EXL3_CHECK_ARG(L.sk_tiles <= kMaxCounters, "%s: %d stream-K tiles exceed the counter region", what, L.sk_tiles);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint16_t* xh = reinterpret_cast<uint16_t*>(ws + kCounterBytes);
+  for (int s = 0; s < nshards; s++) sa.xh[s] = xh + (size_t)s * rows * k;
   GemmPlan plan{L.nct, L.sk_tiles, L.groups, L.ksteps, reinterpret_cast<float*>(ws + L.partial_off),
                 reinterpret_cast<int*>(ws)};
-  uint16_t* xh = reinterpret_cast<uint16_t*>(ws + kCounterBytes);
-  hipStream_t st = as_stream(stream);
-  // input rotation of every shard, in fragment order, one launch
-  ShardSuh su{};
-  for (int s = 0; s < nshards; s++) su.suh[s] = static_cast<const uint16_t*>(shards_host[s].suh);
+  int n_total = 0;
+  for (int s = 0; s < nshards; s++) n_total += shard_n[s];
+  // the input pass: every shard in one launch
   const size_t hunits = (size_t)nshards * rows * (k / 128);
   bool aligned16 = ((uintptr_t)x & 15) == 0;
-  for (int s = 0; s < nshards; s++) aligned16 = aligned16 && ((uintptr_t)su.suh[s] & 15) == 0;
+  if constexpr (ROT)
+    for (int s = 0; s < nshards; s++) aligned16 = aligned16 && ((uintptr_t)su.suh[s] & 15) == 0;
   if (aligned16) {
     const int hu = hunits >= (1u << 17) ? 4 : hunits >= (1u << 15) ? 2 : 1;
     const dim3 hgrid((unsigned)((hunits + 16 * hu - 1) / (16 * hu)));
-    auto frag = x_bf16 ? (hu == 4 ? had_in_frag16_kernel<true, 4> : hu == 2 ? had_in_frag16_kernel<true, 2>
-                                                                            : had_in_frag16_kernel<true, 1>)
-                       : (hu == 4 ? had_in_frag16_kernel<false, 4> : hu == 2 ? had_in_frag16_kernel<false, 2>
-                                                                             : had_in_frag16_kernel<false, 1>);
+    auto frag = x_bf16 ? (hu == 4 ? had_in_frag16_kernel<true, 4, ROT> : hu == 2 ? had_in_frag16_kernel<true, 2, ROT>
+                                                                                 : had_in_frag16_kernel<true, 1, ROT>)
+                       : (hu == 4 ? had_in_frag16_kernel<false, 4, ROT> : hu == 2 ? had_in_frag16_kernel<false, 2, ROT>
+                                                                                  : had_in_frag16_kernel<false, 1, ROT>);
     frag<<<hgrid, 256, 0, st>>>(x, rows, k, su, nshards, xh);
   } else {
     const int hu = hunits >= (1u << 17) ? 4 : 1;
     const dim3 hgrid((unsigned)((hunits + 8 * hu - 1) / (8 * hu)));
-    auto frag = x_bf16 ? (hu == 4 ? had_in_frag_kernel<true, 4> : had_in_frag_kernel<true, 1>)
-                       : (hu == 4 ? had_in_frag_kernel<false, 4> : had_in_frag_kernel<false, 1>);
+    auto frag = x_bf16 ? (hu == 4 ? had_in_frag_kernel<true, 4, ROT> : had_in_frag_kernel<true, 1, ROT>)
+                       : (hu == 4 ? had_in_frag_kernel<false, 4, ROT> : had_in_frag_kernel<false, 1, ROT>);
     frag<<<hgrid, 256, 0, st>>>(x, rows, k, su, nshards, xh);
   }
   EXL3_CHECK_LAUNCH();
@@ -691,7 +696,7 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   bool ok;
 #define EXL3_GEMM_LAUNCH(YB, FEW)                                                                              \
   ok = EXL3_GEMM_DISPATCH(K, codebook, gemm_kernel<kK, kCB, YB, FEW><<<grid, kGemmThreads, kGemmLds, st>>>( \
-                                          sa, plan, rows, k, y, col, 1))
+                                          sa, plan, rows, k, y, n_total, ROT ? 1 : 0))
   const bool few = rows < kBM;  // one row block, mostly rows past M
   if (y_bf16 && few)
     EXL3_GEMM_LAUNCH(true, true);
@@ -702,7 +707,70 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
   else
     EXL3_GEMM_LAUNCH(false, false);
 #undef EXL3_GEMM_LAUNCH
-  if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_linear_prefill: unsupported K/codebook");
+  if (!ok) return set_error(EXL3_ERR_INVALID, "%s: unsupported K/codebook", what);
   EXL3_CHECK_LAUNCH();
   return EXL3_OK;
 }
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host,
+                                   int nshards, int K, int codebook, void* y, int y_bf16, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  EXL3_CHECK_ARG(x && y && shards_host, "exl3_linear_prefill: null pointer");
+  EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_linear_prefill: K = %d / codebook = %d", K, codebook);
+  EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_linear_prefill: rows = %d, k = %d", rows, k);
+  EXL3_CHECK_ARG(nshards >= 1 && nshards <= EXL3_MAX_SHARDS, "exl3_linear_prefill: nshards = %d", nshards);
+  if (rows == 0) return EXL3_OK;
+  EXL3_CHECK_ARG((int64_t)rows * k * 2 <= INT32_MAX, "exl3_linear_prefill: rows * k too large for one launch");
+  GemmShards sa{};
+  ShardSuh su{};
+  int col = 0, ctl = 0;
+  int shard_n[EXL3_MAX_SHARDS];
+  for (int s = 0; s < nshards; s++) {
+    const exl3_shard& sh = shards_host[s];
+    EXL3_CHECK_ARG(sh.trellis && sh.suh && sh.svh, "shard %d: null tensor pointer", s);
+    EXL3_CHECK_ARG(sh.n > 0 && sh.n % 128 == 0, "shard %d: n = %d is not a positive multiple of 128", s, sh.n);
+    EXL3_CHECK_ARG((int64_t)k * sh.n * K / 8 <= INT32_MAX, "shard %d: trellis exceeds the 2 GiB buffer range", s);
+    sa.trellis[s] = static_cast<const uint32_t*>(sh.trellis);
+    sa.svh[s] = static_cast<const uint16_t*>(sh.svh);
+    su.suh[s] = static_cast<const uint16_t*>(sh.suh);
+    sa.tn[s] = sh.n / 16;
+    sa.col0[s] = col;
+    sa.ct0[s] = ctl;
+    shard_n[s] = sh.n;
+    col += sh.n;
+    ctl += (sh.n / 128 + 1) / 2;
+  }
+  sa.ct0[nshards] = ctl;
+  sa.count = nshards;
+  return launch_prefill<true>(x, x_bf16 != 0, rows, k, sa, su, shard_n, K, codebook, y, y_bf16 != 0, workspace,
+                              workspace_bytes, as_stream(stream), "exl3_linear_prefill");
+}
+
+namespace exl3 {
+
+size_t prefill_plain_workspace_bytes(int rows, int k, int n) {
+  const int nct = (n / 128 + 1) / 2;
+  return gemm_layout(rows, k, nct, 1).total;
+}
+
+// exl3_gemm_rotated from kPrefillRows rows: the rows as given (fp16, already in the rotated basis), no output
+// rotation, so one-hot rows read W_inner back through the decode-GEMM bit for bit
+int prefill_plain_gemm(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook, void* out,
+                       void* workspace, size_t workspace_bytes, hipStream_t st) {
+  EXL3_CHECK_ARG((int64_t)rows * k * 2 <= INT32_MAX, "exl3_gemm_rotated: rows * k too large for one launch");
+  GemmShards sa{};
+  sa.trellis[0] = static_cast<const uint32_t*>(trellis);
+  sa.tn[0] = n / 16;
+  sa.ct0[1] = (n / 128 + 1) / 2;
+  sa.count = 1;
+  const ShardSuh su{};
+  const int shard_n[1] = {n};
+  return launch_prefill<false>(xh, false, rows, k, sa, su, shard_n, K, codebook, out, false, workspace,
+                               workspace_bytes, st, "exl3_gemm_rotated");
+}
+
+}  // namespace exl3

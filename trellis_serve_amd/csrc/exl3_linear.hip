@@ -221,30 +221,29 @@ constexpr int kGemvThreads = kGemvWaves * 64;
 constexpr int kCoherentDevice = 1 << 4;  // buffer cache policy sc1: device-scope coherent access
 constexpr int kWaitVmcnt0 = 0x0F70;      // s_waitcnt vmcnt(0) (expcnt, lgkmcnt unconstrained)
 
-// LDS bytes of the GEMV: staged activations (M rows of NT*16 + 4 halves, or twice that with every value staged
-// twice: NT*32 + 8), then per wave two block stages of 256*K bytes; at least 16 * 128 fp32 for the epilogue reduce
-__host__ __device__ constexpr int gemv_mstride(int NT, bool dup) { return dup ? NT * 32 + 8 : NT * 16 + 4; }
-__host__ __device__ constexpr int gemv_a_bytes(int M, int NT, bool dup) {
-  return ((M * gemv_mstride(NT, dup) * 2) + 15) & ~15;
-}
-__host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K, bool dup) {
-  return gemv_a_bytes(M, NT, dup) + kGemvWaves * stream_lds_bytes(K) > kGemvThreads * 16
-             ? gemv_a_bytes(M, NT, dup) + kGemvWaves * stream_lds_bytes(K)
+// LDS bytes of the GEMV: staged activations (M rows of a_mstride(NT) halves), then per wave two block stages of 256*K
+// bytes; at least 16 * 128 fp32 for the epilogue reduce
+__host__ __device__ constexpr int gemv_a_bytes(int M, int NT) { return ((M * a_mstride(NT) * 2) + 15) & ~15; }
+__host__ __device__ constexpr int gemv_lds_bytes(int M, int NT, int K) {
+  return gemv_a_bytes(M, NT) + kGemvWaves * stream_lds_bytes(K) > kGemvThreads * 16
+             ? gemv_a_bytes(M, NT) + kGemvWaves * stream_lds_bytes(K)
              : kGemvThreads * 16;
 }
 
-// PRE: x is the rotated activations of every shard, [shards][pre_rows][k] in A-staging order (had_in_kernel<.., true>),
-// staged by plain 8-byte copies; else x is the input rows, rotated here (ROTATE) or taken as given
-// P = 2 / 4 (17-32 / 33-64 rows): every decoded tile feeds P 16-row MFMA groups (rounded fp16 weights, v_mfma
-// 16x16x16): the weights stream once for 16 P rows instead of once per 16.  The staged rows are padded with zeros.
+// PRE: x is the rotated activations of every shard, [shards][pre_rows][k] in A-staging order (had_in_shards_kernel),
+// staged by 8-byte copies; else x is the input rows, rotated here (ROTATE) or taken as given.
+// Every decoded tile pair feeds one v_mfma_f32_16x16x32_f16 per 16-row group: P = 1 up to 16 rows
+// (TileStream::run_pairs), P = 2 / 4 for 17-32 / 33-64 rows (run_groups: the weights stream once for 16 P rows
+// instead of once per 16; the staged rows are padded with zeros).  Every form multiplies by the rounded fp16 weights
+// of trellis_core.
 template <int K, int CB, bool ROTATE, int NT, bool PRE = false, int P = 1>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
                                                              int M, int k, int splits, float* partial,
                                                              int* counters, void* __restrict__ y,
                                                              int y_bf16, int n_total, int pre_rows = 0) {
-  typedef TileStream<K, CB, NT, false, P == 1> Stream;
+  typedef TileStream<K, CB, NT, false> Stream;
   constexpr int NB = Stream::NB;
-  constexpr bool DUP = Stream::DUP;  // activations staged twice for the two-halves decode (MCG, 3INST, one group)
+
   const int Mp = P == 1 ? M : kGemvRows * ((M + kGemvRows - 1) / kGemvRows);  // staged rows; rows M .. Mp-1 are 0
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
@@ -254,14 +253,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   const ShardView sh = shard_of_block(sa, blk);
   const int kb0 = split * NB;
   const int nb = min(k >> 7, kb0 + NB) - kb0;  // blocks of this split holding data (1..NB)
-  constexpr int mstride = gemv_mstride(NT, DUP);
-  // one activation value into the staging area (twice with DUP: a_slot_dup is 2 a_slot inside a row)
-  auto stage1 = [&](int p, int m, _Float16 h) {
-    if constexpr (DUP)
-      *reinterpret_cast<half2_t*>(xs + a_slot_dup(p, m, mstride)) = half2_t{h, h};
-    else
-      xs[a_slot(p, m, mstride)] = h;
-  };
+  constexpr int mstride = a_mstride(NT);
+  auto stage1 = [&](int p, int m, _Float16 h) { xs[a_slot(p, m, mstride)] = h; };  // one activation value
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
@@ -285,7 +278,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
   Stream stream;
   stream.init(sh.trellis, (k >> 4) * tn * 32 * K, tn, (blk - sh.blk0) * kGemvWaves + w, kb0, nb,
-              lds + gemv_a_bytes(Mp, NT, DUP) + w * Stream::LDS_BYTES, l);
+              lds + gemv_a_bytes(Mp, NT) + w * Stream::LDS_BYTES, l);
   // Trellis blocks issued before the prologue.  Every workgroup's activation loads queue behind the trellis loads
   // the CU's workgroups issued before them, so the prologue (and with it the first MFMA) waits less with fewer early
   // blocks; the rest of the three in flight follow the prologue's barrier (layer set at one row: 79.2 -> 78.2 us).
@@ -311,15 +304,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
       const int u = hw + it * 2 * kGemvWaves;
       const int m = u / NB, b = u - m * NB;
       if (u < Mp * NB) {  // rows M .. Mp-1 store the zeros v was set to
-        if constexpr (DUP) {  // the 4 staged halves, each twice
-          uint32_t d[4] = {__builtin_amdgcn_perm(v[it].x, v[it].x, 0x01000100u),
-                           __builtin_amdgcn_perm(v[it].x, v[it].x, 0x03020302u),
-                           __builtin_amdgcn_perm(v[it].y, v[it].y, 0x01000100u),
-                           __builtin_amdgcn_perm(v[it].y, v[it].y, 0x03020302u)};
-          *reinterpret_cast<u32x4_t*>(xs + m * mstride + b * 256 + 8 * t) = u32x4_t{d[0], d[1], d[2], d[3]};
-        } else {
-          *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
-        }
+        *reinterpret_cast<uint2_t*>(xs + m * mstride + b * 128 + 4 * t) = v[it];
       }
     }
   } else if (single) {
@@ -369,12 +354,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   if constexpr (P > 1) {
 #pragma unroll
     for (int p = 0; p < P; p++) acc[p] = float4_t{0.f, 0.f, 0.f, 0.f};
-    stream.template run_groups<P>(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j,
-                                  kGemvRows * mstride / 4, Mp / kGemvRows, acc);
-  } else if constexpr (DUP) {
-    acc[0] = stream.run_dup(reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j);
+    stream.template run_groups<P>(reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j,
+                                  kGemvRows * mstride / 8, Mp / kGemvRows, acc);
   } else {
-    acc[0] = stream.run(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j);
+    acc[0] = stream.run_pairs(reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j);
   }
 
 
@@ -472,11 +455,10 @@ static int gemv_target_wgs() {
 }
 
 // pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there.
-// cb: MCG / 3INST stage the activations twice (more LDS per tile row) when one row group serves the launch; past 16
-// rows (two groups, P = 2) the activations are staged once, padded to 32 rows
-static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = false) {
+// Past 16 rows (P = 2, 4) the staged activations are padded to 32 or 64 rows.  The plan does not depend on the
+// codebook.
+static GemvPlan gemv_plan(int k, int n_total, int M, int K, bool pre = false) {
   const int kb = k / 128, nblk = n_total / 128;
-  const bool dup = cb != CB_MUL1 && M <= kGemvRows;
   const int Ms = M <= kGemvRows ? M : M <= kGemvPairRows ? kGemvPairRows : kGemvQuadRows;
   int nt = 16;
   if (M <= kGemvRows) {
@@ -489,22 +471,22 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K, int cb, bool pre = f
       if (pre && cand != 32) continue;
       const int nbc = cand / 8, splits = (kb + nbc - 1) / nbc;
       if (splits * nbc * 50 <= kb * 51 && (size_t)nblk * splits >= kGemvOneGroupWgs &&
-          gemv_lds_bytes(Ms, cand, K, dup) <= kGemvMaxLds) {
+          gemv_lds_bytes(Ms, cand, K) <= kGemvMaxLds) {
         nt = cand;
         break;
       }
     }
-    return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(Ms, nt, K, dup)};
+    return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(Ms, nt, K)};
   }
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
     if (pre && cand > 32) continue;
-    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs() && gemv_lds_bytes(Ms, cand, K, dup) <= kGemvMaxLds) {
+    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs() && gemv_lds_bytes(Ms, cand, K) <= kGemvMaxLds) {
       nt = cand;
       break;
     }
   }
-  return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(Ms, nt, K, dup)};
+  return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(Ms, nt, K)};
 }
 
 // workspace layout: [counter region: one int per 128-column block, zero between calls][fp32 partials]; the region
@@ -579,19 +561,18 @@ static int gemv_launch_rows(int k, int n_total, int launch_rows) {
   return (size_t)nblk * ((kb + 3) / 4) < (size_t)gemv_target_wgs() ? kGemvQuadRows : kGemvPairRows;
 }
 
-// workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre]; the size does
-// not depend on the codebook (the largest plan of either staging form).  launch_rows: the caller's rows per launch,
-// 16, or 64 where row groups share each decoded tile (exl3_linear; gemv_launch_rows may lower it to 32)
+// workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre].
+// launch_rows: the entry point's rows per launch, 16 (exl3_gemm_rotated, exl3_linear_noalloc), or 64 where row groups
+// share each decoded tile (exl3_linear; gemv_launch_rows may lower it to 32).  A call's launches are the full ones
+// and the remainder, each with its own split plan: the partial region holds the larger of the two.
+static size_t gemv_launch_partial_bytes(int M, int rows, int k, int n_total, int K) {
+  return (size_t)gemv_plan(k, n_total, M, K, gemv_pre(rows, k, n_total)).splits * M * n_total * sizeof(float);
+}
 static size_t gemv_partial_bytes(int rows, int k, int n_total, int K, int launch_rows) {
   size_t need = 0;
   launch_rows = gemv_launch_rows(k, n_total, launch_rows);
-  for (int M : {std::min(rows, launch_rows), rows % launch_rows}) {
-    if (M == 0) continue;
-    for (int cb : {(int)CB_MCG, (int)CB_MUL1}) {
-      const GemvPlan pl = gemv_plan(k, n_total, M, K, cb, gemv_pre(rows, k, n_total));
-      need = std::max(need, (size_t)pl.splits * M * n_total * sizeof(float));
-    }
-  }
+  for (int M : {std::min(rows, launch_rows), rows % launch_rows})
+    if (M > 0) need = std::max(need, gemv_launch_partial_bytes(M, rows, k, n_total, K));
   return (need + 255) & ~(size_t)255;
 }
 static size_t gemv_pre_bytes(int rows, int k, int n_total) {
@@ -603,9 +584,16 @@ static size_t gemv_workspace_bytes(int rows, int k, int n_total, int K, int laun
          gemv_pre_bytes(rows, k, n_total);
 }
 
-// launch_rows: 64 (two or four row groups per decoded tile past 16 rows; rotated launches only) or 16
+// launch_rows: 64 (two or four row groups per decoded tile past 16 rows; rotated launches only) or 16.  The
+// workspace is checked here against the plans of exactly these launches (every entry point's size function sizes the
+// same plans): a short workspace returns EXL3_ERR_INVALID before anything is launched.
 static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_bf16, int rows, int k, int K, int cb,
-                       int n_total, void* workspace, void* y, bool y_bf16, hipStream_t st, int launch_rows) {
+                       int n_total, void* workspace, size_t workspace_bytes, void* y, bool y_bf16, hipStream_t st,
+                       int launch_rows, const char* what) {
+  const size_t need = gemv_workspace_bytes(rows, k, n_total, K, launch_rows);
+  EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "%s: workspace %zu bytes, need %zu", what, workspace_bytes,
+                 need);
+  const size_t partial_room = gemv_partial_bytes(rows, k, n_total, K, launch_rows);
   int* counters = static_cast<int*>(workspace);
   float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total));
   const bool pre = rotate && gemv_pre(rows, k, n_total);
@@ -624,7 +612,10 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
     const int M = std::min(launch_rows, rows - r0);
     // two or four row groups per decoded tile (rotated launches only: launch_rows is 16 otherwise)
     const bool quad = M > kGemvPairRows, pair = M > kGemvRows && !quad;
-    const GemvPlan pl = gemv_plan(k, n_total, M, K, cb, pre);
+    const GemvPlan pl = gemv_plan(k, n_total, M, K, pre);
+    EXL3_CHECK_ARG((size_t)pl.splits * M * n_total * sizeof(float) <= partial_room,
+                   "%s: a launch of %d rows needs %zu bytes of partials, the workspace plan holds %zu", what, M,
+                   (size_t)pl.splits * M * n_total * sizeof(float), partial_room);
     const dim3 grid(n_total / 128, pl.splits);
     const void* xr = static_cast<const uint8_t*>(pre ? (const void*)xh : x) + (size_t)r0 * k * 2;
     void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
@@ -711,16 +702,24 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int n) {
   if (i < n) p[i] = 0u;
 }
 
-// The current device's scratch address, looked up (and its counter region cleared by a fill kernel on `st`) on the
-// first call for that device.  Every GEMV call leaves its counters at zero again, so clearing once is enough.
-static int scratch_of_current_device(hipStream_t st, void** out) {
-  int dev = 0;
-  EXL3_CHECK_HIP(hipGetDevice(&dev));
+// The scratch address on the device that `st` belongs to (the current device for the null stream), looked up (and
+// its counter region cleared by a fill kernel on `st`) on the first call for that device.  The lookup runs with that
+// device current, since hipGetSymbolAddress answers for the current device.  Every GEMV call leaves its counters at
+// zero again, so clearing once is enough.
+static int scratch_of_stream_device(hipStream_t st, void** out) {
+  int cur = 0, dev = 0;
+  EXL3_CHECK_HIP(hipGetDevice(&cur));
+  dev = cur;
+  if (st != nullptr) EXL3_CHECK_HIP(hipStreamGetDevice(st, &dev));
   EXL3_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "exl3_linear_noalloc: device %d beyond %d", dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch[dev] == nullptr) {
+    if (dev != cur) EXL3_CHECK_HIP(hipSetDevice(dev));
     void* p = nullptr;
-    EXL3_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) EXL3_CHECK_HIP(hipSetDevice(cur));
+    if (e != hipSuccess)
+      return set_error(EXL3_ERR_HIP, "exl3_linear_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
     EXL3_CHECK_ARG(p != nullptr, "exl3_linear_noalloc: no device address for the scratch array");
     const int words = (int)(kCounterBytes / 4);
     zero_words_kernel<<<dim3((unsigned)((words + 255) / 256)), 256, 0, st>>>(static_cast<uint32_t*>(p), words);
@@ -804,10 +803,10 @@ extern "C" int exl3_had_out_into(const void* y, int rows, int n, const void* svh
 }
 
 extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int K) {
-  (void)K;
-  if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128 || n_total / 128 > kMaxCounters) return 0;
-  // launches take 64 rows at a time (16 for exl3_gemm_rotated: its need is no larger), then the remainder: the
-  // workspace holds either plan's partials
+  if (rows <= 0 || k <= 0 || n_total <= 0 || k % 128 || n_total % 128 || n_total / 128 > kMaxCounters ||
+      !valid_bits(K))
+    return 0;
+  // exl3_linear's launches: up to 64 rows each (1, 2 or 4 row groups per decoded tile), then the remainder
   return gemv_workspace_bytes(rows, k, n_total, K, kGemvQuadRows);
 }
 
@@ -821,13 +820,18 @@ extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl
   int n_total = 0;
   if (int rc = build_shards(shards_host, nshards, k, K, &sa, &n_total)) return rc;
   if (rows == 0) return EXL3_OK;
-  const size_t need = exl3_linear_workspace_bytes(rows, k, n_total, K);
-  EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_linear: workspace %zu bytes, need %zu", workspace_bytes,
-                 need);
-  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, workspace, y, y_bf16 != 0,
-                     as_stream(stream), kGemvQuadRows);
+  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, workspace, workspace_bytes, y,
+                     y_bf16 != 0, as_stream(stream), kGemvQuadRows, "exl3_linear");
 }
 
+extern "C" size_t exl3_gemm_rotated_workspace_bytes(int rows, int k, int n, int K) {
+  if (rows <= 0 || k <= 0 || n <= 0 || k % 128 || n % 128 || n / 128 > kMaxCounters || !valid_bits(K)) return 0;
+  if (rows >= kPrefillRows) return prefill_plain_workspace_bytes(rows, k, n);
+  return gemv_workspace_bytes(rows, k, n, K, kGemvRows);
+}
+
+// Rows are served by the kernel that serves the same row count in a linear: below kPrefillRows the decode-GEMV (one
+// 16-row group per launch, two decoded tiles per MFMA), from there the prefill decode-GEMM, both without rotations.
 extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook,
                                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
   EXL3_CHECK_ARG(xh && trellis && out, "exl3_gemm_rotated: null pointer");
@@ -837,16 +841,16 @@ extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* tr
   EXL3_CHECK_ARG((int64_t)k * n * K / 8 <= INT32_MAX, "exl3_gemm_rotated: trellis exceeds the 2 GiB buffer range");
   EXL3_CHECK_ARG(n / 128 <= kMaxCounters, "exl3_gemm_rotated: n = %d exceeds %d columns", n, kMaxCounters * 128);
   if (rows == 0) return EXL3_OK;
-  const size_t need = exl3_linear_workspace_bytes(rows, k, n, K);
-  EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_gemm_rotated: workspace %zu bytes, need %zu",
-                 workspace_bytes, need);
+  if (rows >= kPrefillRows)
+    return prefill_plain_gemm(xh, rows, k, trellis, n, K, codebook, out, workspace, workspace_bytes,
+                              as_stream(stream));
   ShardArgs sa{};
   sa.trellis[0] = static_cast<const uint32_t*>(trellis);
   sa.tn[0] = n / 16;
   sa.blk0[1] = n / 128;
   sa.count = 1;
-  return launch_gemv(sa, xh, false, false, rows, k, K, codebook, n, workspace, out, false, as_stream(stream),
-                     kGemvRows);
+  return launch_gemv(sa, xh, false, false, rows, k, K, codebook, n, workspace, workspace_bytes, out, false,
+                     as_stream(stream), kGemvRows, "exl3_gemm_rotated");
 }
 
 extern "C" size_t exl3_linear_noalloc_max_bytes(void) { return EXL3_NOALLOC_SCRATCH_BYTES; }
@@ -867,6 +871,7 @@ extern "C" int exl3_linear_noalloc(const void* x, int x_bf16, int rows, int k, c
                  "exl3_linear with a workspace", rows, k, n_total, need, (size_t)EXL3_NOALLOC_SCRATCH_BYTES);
   hipStream_t st = as_stream(stream);
   void* ws = nullptr;
-  if (int rc = scratch_of_current_device(st, &ws)) return rc;
-  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, ws, y, y_bf16 != 0, st, kGemvRows);
+  if (int rc = scratch_of_stream_device(st, &ws)) return rc;
+  return launch_gemv(sa, x, true, x_bf16 != 0, rows, k, K, codebook, n_total, ws, EXL3_NOALLOC_SCRATCH_BYTES, y,
+                     y_bf16 != 0, st, kGemvRows, "exl3_linear_noalloc");
 }

@@ -66,11 +66,11 @@ struct MoeArgs {
 template <int P, bool PRE>
 __host__ __device__ constexpr int moe_act_buffers() { return PRE && P != 2 ? 2 : 1; }
 
-// LDS: staged activations [16 P rows][NT*16 + 4 halves] x moe_act_buffers, then per wave the stream stages.  P groups
-// of 16 slots share each decoded tile.
+// LDS: staged activations [16 P rows][a_mstride(NT) halves] x moe_act_buffers, then per wave the stream stages.  P
+// groups of 16 slots share each decoded tile pair.
 template <int K, int P, int NT, bool PRE>
 __host__ __device__ constexpr int moe_lds_bytes() {
-  return moe_act_buffers<P, PRE>() * kMoeRows * P * (NT * 16 + 4) * 2 + kMoeWaves * stream_lds_bytes(K, PRE);
+  return moe_act_buffers<P, PRE>() * kMoeRows * P * a_mstride(NT) * 2 + kMoeWaves * stream_lds_bytes(K, PRE);
 }
 
 static_assert(moe_lds_bytes<8, 4, 16, true>() <= 160 * 1024, "MoE LDS must fit a CU");
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
-  const int mstride = NT * 16 + 4;
+  constexpr int mstride = a_mstride(NT);
 
   // expert and its slots: routed mode -- grid row = active expert, its slot list from the routing launch; slot mode
   // -- grid row = slot, one slot, its expert read from topk_ids (split counters then index slots, so repeated experts
@@ -320,8 +320,8 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
       };
       _Float16* xs1 = kActBufs == 2 ? xs + kMoeRows * P * mstride : xs;
       // A row of lane group c in group p: 16 p + c (group 0: min(c, M - 1)); rows >= M feed only C rows never stored
-      const half4_t* ap0 = reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j;
-      const half4_t* ap1 = reinterpret_cast<const half4_t*>(xs1 + min(c, M - 1) * mstride) + j;
+      const half8_t* ap0 = reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j;
+      const half8_t* ap1 = reinterpret_cast<const half8_t*>(xs1 + min(c, M - 1) * mstride) + j;
       Stream s0, s1;
       uint2_t v[IT];
       load_a(0, v);
@@ -334,19 +334,19 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
       for (; ch + 2 <= nch; ch += 2) {
         load_a(ch + 1, v);
         start(s1, ch + 1);
-        s0.template run_groups<P>(ap0, kMoeRows * mstride / 4, groups, acc);
+        s0.template run_groups<P>(ap0, kMoeRows * mstride / 8, groups, acc);
         if constexpr (kActBufs == 1) lds_barrier();  // one buffer: every wave is done with chunk ch
         store_a(xs1, v);
         lds_barrier();  // chunk ch + 1 staged; every wave is done with buffer 0
         load_a(ch + 2, v);
         start(s0, ch + 2);
-        s1.template run_groups<P>(ap1, kMoeRows * mstride / 4, groups, acc);
+        s1.template run_groups<P>(ap1, kMoeRows * mstride / 8, groups, acc);
         if constexpr (kActBufs == 1) lds_barrier();
         store_a(xs, v);
         lds_barrier();
       }
       if (ch < nch) {  // the odd last chunk: staged in buffer 0, its blocks in stream 0
-        s0.template run_groups<P>(ap0, kMoeRows * mstride / 4, groups, acc);
+        s0.template run_groups<P>(ap0, kMoeRows * mstride / 8, groups, acc);
         lds_barrier();
       }
     } else {
@@ -371,8 +371,8 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
         }
         __syncthreads();
         // A row of lane group c in group p: 16 p + c (group 0: min(c, M - 1)); rows >= M feed only C rows never stored
-        stream.template run_groups<P>(reinterpret_cast<const half4_t*>(xs + min(c, M - 1) * mstride) + j,
-                                      kMoeRows * mstride / 4, groups, acc);
+        stream.template run_groups<P>(reinterpret_cast<const half8_t*>(xs + min(c, M - 1) * mstride) + j,
+                                      kMoeRows * mstride / 8, groups, acc);
         __syncthreads();  // the next chunk or pass restages LDS
       }
     }

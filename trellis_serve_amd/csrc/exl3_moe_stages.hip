@@ -29,7 +29,7 @@ namespace exl3 {
 
 constexpr int kStageWaves = 8, kStageThreads = kStageWaves * 64;
 constexpr int kStageNT = 16;                     // tile rows per chunk: NB = 2 blocks of 128 input rows
-constexpr int kStageMStride = kStageNT * 16 + 4;  // staged activation row stride (halves)
+constexpr int kStageMStride = a_mstride(kStageNT);  // staged activation row stride (halves)
 constexpr int kAlignThreads = 1024, kAlignMaxExperts = 1024;
 
 struct StageStacks {
@@ -152,13 +152,13 @@ template <int K, int CB, int P>
 __global__ __launch_bounds__(kStageThreads) void moe_block_gemm_kernel(
     StageStacks st, const uint16_t* __restrict__ a, int rows, int k, int n, int shards, const int* __restrict__ sorted,
     const int* __restrict__ eids, const int* __restrict__ post, int block, int E, uint16_t* __restrict__ c,
-    float* partial, int* counters, int splits, int chunks) {
+    float* partial, int* counters, int splits, int chunks, int bi0) {
   typedef TileStream<K, CB, kStageNT> Stream;
   constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
   _Float16* xs = reinterpret_cast<_Float16*>(lds);
-  const int bi = blockIdx.y;
+  const int bi = bi0 + blockIdx.y;  // align block; this launch covers blocks bi0 .. bi0 + gridDim.y - 1
   if (bi * block >= *post) return;
   const int e = eids[bi];
   if (e < 0 || e >= E) return;
@@ -199,8 +199,8 @@ __global__ __launch_bounds__(kStageThreads) void moe_block_gemm_kernel(
       for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, kStageMStride)] = v[i];
     }
     __syncthreads();
-    stream.template run_groups<P>(reinterpret_cast<const half4_t*>(xs + cl * kStageMStride) + j,
-                                  16 * kStageMStride / 4, groups, acc);
+    stream.template run_groups<P>(reinterpret_cast<const half8_t*>(xs + cl * kStageMStride) + j,
+                                  16 * kStageMStride / 8, groups, acc);
     __syncthreads();  // the next chunk restages LDS
   }
   // this split's partial rows (lane: rows 16 p + 4 j + r, column cl of the wave's 16), device-coherent: read by the
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kStageThreads) void moe_block_gemm_kernel(
                                            __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-  const int ctr = bi * (shards * ncb) + cb;
+  const int ctr = blockIdx.y * (shards * ncb) + cb;  // counters are per launch: launches are ordered on the stream
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -340,7 +340,7 @@ extern "C" int exl3_moe_had_in(const void* x, int x_bf16, int tokens, int k, con
 
 extern "C" size_t exl3_moe_gemm_workspace_bytes(int rows, int k, int n, int shards, int max_blocks) {
   if (rows <= 0 || k <= 0 || k % 128 || n <= 0 || n % 128 || shards < 1 || shards > 2 || max_blocks <= 0) return 0;
-  if ((int64_t)max_blocks * shards * (n / 128) > kMaxCounters) return 0;
+  if (shards * (n / 128) > kMaxCounters) return 0;
   return stage_plan(rows, k, n, shards, max_blocks).total;
 }
 
@@ -359,8 +359,7 @@ extern "C" int exl3_moe_gemm(const void* a, int rows, int k, const void* const* 
                  "exl3_moe_gemm: block = %d (1..64), max_blocks = %d, num_experts = %d", block, max_blocks,
                  num_experts);
   EXL3_CHECK_ARG((int64_t)k * n * K / 8 <= INT32_MAX, "exl3_moe_gemm: expert matrix exceeds the 2 GiB buffer range");
-  EXL3_CHECK_ARG((int64_t)max_blocks * shards * (n / 128) <= kMaxCounters,
-                 "exl3_moe_gemm: %d blocks x %d column blocks exceed the counter region", max_blocks,
+  EXL3_CHECK_ARG(shards * (n / 128) <= kMaxCounters, "exl3_moe_gemm: %d column blocks exceed the counter region",
                  shards * (n / 128));
   EXL3_CHECK_ARG((int64_t)rows * shards * n <= INT32_MAX / 8, "exl3_moe_gemm: too many rows");
   if (rows == 0) return EXL3_OK;
@@ -375,26 +374,34 @@ extern "C" int exl3_moe_gemm(const void* a, int rows, int k, const void* const* 
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   float* partial = reinterpret_cast<float*>(ws + p.partial_off);
   int* counters = reinterpret_cast<int*>(ws);
-  const dim3 grid((unsigned)(shards * (n / 128)), (unsigned)max_blocks, (unsigned)p.splits);
   hipStream_t s = as_stream(stream);
   const uint16_t* av = static_cast<const uint16_t*>(a);
   uint16_t* cv = static_cast<uint16_t*>(c);
-  const bool ok = EXL3_STAGE_DISPATCH(K, codebook, {
-    if (block <= 16)
-      moe_block_gemm_kernel<kK, kCB, 1><<<grid, kStageThreads, stage_lds_bytes<kK, 1>(), s>>>(
-          st, av, rows, k, n, shards, sorted_ids, expert_ids, num_post_padded, block, num_experts, cv, partial,
-          counters, p.splits, p.chunks);
-    else if (block <= 32)
-      moe_block_gemm_kernel<kK, kCB, 2><<<grid, kStageThreads, stage_lds_bytes<kK, 2>(), s>>>(
-          st, av, rows, k, n, shards, sorted_ids, expert_ids, num_post_padded, block, num_experts, cv, partial,
-          counters, p.splits, p.chunks);
-    else
-      moe_block_gemm_kernel<kK, kCB, 4><<<grid, kStageThreads, stage_lds_bytes<kK, 4>(), s>>>(
-          st, av, rows, k, n, shards, sorted_ids, expert_ids, num_post_padded, block, num_experts, cv, partial,
-          counters, p.splits, p.chunks);
-  });
-  if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_moe_gemm: unsupported K = %d / codebook = %d", K, codebook);
-  EXL3_CHECK_LAUNCH();
+  // One counter per (align block, column block) of a launch: align blocks go out in launches of at most
+  // kMaxCounters / column blocks each (one launch up to 65536 / 32 = 2048 blocks at H = 4096, two column shards).
+  // Launches are ordered on the stream and every launch leaves its counters at zero, so the next reuses them; a row
+  // belongs to one block, so launches never share partial rows.
+  const int per_launch = kMaxCounters / (shards * (n / 128));
+  for (int b0 = 0; b0 < max_blocks; b0 += per_launch) {
+    const dim3 grid((unsigned)(shards * (n / 128)), (unsigned)std::min(per_launch, max_blocks - b0),
+                    (unsigned)p.splits);
+    const bool ok = EXL3_STAGE_DISPATCH(K, codebook, {
+      if (block <= 16)
+        moe_block_gemm_kernel<kK, kCB, 1><<<grid, kStageThreads, stage_lds_bytes<kK, 1>(), s>>>(
+            st, av, rows, k, n, shards, sorted_ids, expert_ids, num_post_padded, block, num_experts, cv, partial,
+            counters, p.splits, p.chunks, b0);
+      else if (block <= 32)
+        moe_block_gemm_kernel<kK, kCB, 2><<<grid, kStageThreads, stage_lds_bytes<kK, 2>(), s>>>(
+            st, av, rows, k, n, shards, sorted_ids, expert_ids, num_post_padded, block, num_experts, cv, partial,
+            counters, p.splits, p.chunks, b0);
+      else
+        moe_block_gemm_kernel<kK, kCB, 4><<<grid, kStageThreads, stage_lds_bytes<kK, 4>(), s>>>(
+            st, av, rows, k, n, shards, sorted_ids, expert_ids, num_post_padded, block, num_experts, cv, partial,
+            counters, p.splits, p.chunks, b0);
+    });
+    if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_moe_gemm: unsupported K = %d / codebook = %d", K, codebook);
+    EXL3_CHECK_LAUNCH();
+  }
   return EXL3_OK;
 }
 

@@ -9,9 +9,11 @@
 // registers, exact in-order vmcnt waits.  A stream shorter than NT rows (a split's tail) clamps its loads to its
 // last block; the caller gives it zero activations past its end.
 //
-// Every decoded tile feeds one MFMA 16x16x16 f16 whose A operand (the activations, staged in LDS by the caller in
-// the same row order as the decoded group: rows 2q, 2q+1, 2q+8, 2q+9 for k-chunk q) is read at a 32-byte step per
-// tile row.
+// Decoded tiles are rounded fp16 weights, bit-identical to trellis_core's (reference.py:52-73; the reference kernel's
+// __hadd, codebook.cuh:56-75).  Two consecutive tiles of the wave's column feed one MFMA 16x16x32 f16 per 16-row
+// group: the lane's 4 weights of tile 2v and its 4 of tile 2v+1 are the 8-half B fragment, against the activations
+// staged by the caller in the matching order (a_slot).  On gfx950 a 16x16x16 f16 MFMA takes as many cycles as a
+// 16x16x32 one, so one MFMA per tile pair is half the matrix-core time of one per tile.
 #pragma once
 #include "exl3_device.hpp"
 
@@ -30,15 +32,8 @@ __host__ __device__ constexpr int stream_lds_bytes(int K, bool all_lanes = false
 // must assume taken or skipped, which turns its in-order load waits into vmcnt(0) in a loop that keeps loads in
 // flight across iterations (the MoE chunk pipeline); straight-line callers (the dense GEMV) keep the lane mask, which
 // spends fewer address cycles (48 of 64 lanes at K = 3).
-// HALVES (the dense GEMV): MCG and 3INST tiles go to the matrix core as their unsummed fp16 halves
-// (decode_group_halves, v_mfma_f32_16x16x32_f16) against activations staged twice (a_slot_dup); MUL1 tiles, and every
-// tile without HALVES, as rounded fp16 weights (v_mfma_f32_16x16x16_f16, a_slot).
-template <int CB, bool HALVES>
-__host__ __device__ constexpr bool stream_dup() { return HALVES && CB != CB_MUL1; }
-
-template <int K, int CB, int NT, bool ALL_LANES = false, bool HALVES = false>
+template <int K, int CB, int NT, bool ALL_LANES = false>
 struct TileStream {
-  static constexpr bool DUP = stream_dup<CB, HALVES>();
   static constexpr int NB = NT / 8;               // 128-row blocks
   static constexpr int CHUNKS = 16 * K;           // 16-byte chunks in the 8 tiles of one block column
   static constexpr int LPB = (CHUNKS + 63) / 64;  // wave-wide gathers per block
@@ -95,9 +90,11 @@ struct TileStream {
     if constexpr (NB > 2) issue(2);
   }
 
-  // ap: the lane's A fragment for tile row 0 (step: 4 half4 per tile row).  Returns the 16 x 16 fp32 C tile slice
-  // (lane l: rows 4(l/16)..+3, column l%16).
-  __device__ __forceinline__ float4_t run(const half4_t* ap) {
+  // One row group: ap is the lane's 8-half A fragment of tile rows 0 and 1 (a_slot order), 4 half8 per tile-row
+  // pair; two accumulators alternate so that consecutive MFMAs do not wait for each other.  Returns the 16 x 16 fp32
+  // C tile slice (lane l: rows 4(l/16)..+3, column l%16).
+  __device__ __forceinline__ float4_t run_pairs(const half8_t* ap) {
+    static_assert(NT % 2 == 0, "tile-row pairs");
     float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -108,46 +105,24 @@ struct TileStream {
       if (b + 3 < NB) issue(b + 3);
       const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const half4_t bv = decode_group<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
-        if (u & 1)
-          acc1 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc1, 0, 0, 0);
+      for (int v = 0; v < 4; v++) {
+        const uint32_t* t0 = tw + 2 * v * 8 * K;
+        const half8_t bv = decode_two_groups<K, CB>(t0[g.dw0], t0[g.dw1], t0[8 * K + g.dw0], t0[8 * K + g.dw1], g);
+        if (v & 1)
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[(b * 4 + v) * 4], bv, acc1, 0, 0, 0);
         else
-          acc0 = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[(b * 8 + u) * 4], bv, acc0, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[(b * 4 + v) * 4], bv, acc0, 0, 0, 0);
       }
     }
     return acc0 + acc1;
   }
 
-  // DUP form of run: ap is the lane's 8-half A fragment ([a, a] per row, a_slot_dup) for tile row 0, 4 half8 per
-  // tile row.
-  __device__ __forceinline__ float4_t run_dup(const half8_t* ap) {
-    float4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-      uint8_t* st = stage + (b & 1) * STAGE;
-#pragma unroll
-      for (int i = 0; i < LPB; i++)
-        if (ALL_LANES || glive[i]) *reinterpret_cast<u32x4_t*>(st + 16 * (i * 64 + lane)) = buf[b][i];
-      if (b + 3 < NB) issue(b + 3);
-      const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const half8_t bv = decode_group_halves<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
-        if (u & 1)
-          acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[(b * 8 + u) * 4], bv, acc1, 0, 0, 0);
-        else
-          acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[(b * 8 + u) * 4], bv, acc0, 0, 0, 0);
-      }
-    }
-    return acc0 + acc1;
-  }
-
-  // For up to P groups of 16 A rows sharing each decoded tile (groups <= P active, uniform): group p reads its
-  // fragment gstride half4 after group p-1's and accumulates into acc[p] (one chain per group: the decode between two
-  // MFMAs of a group covers their dependency).
+  // For up to P groups of 16 A rows sharing each decoded tile pair (groups <= P active, uniform): group p reads its
+  // 8-half fragment gstride half8 after group p-1's and accumulates into acc[p] (one chain per group: the decode
+  // between two MFMAs of a group covers their dependency).
   template <int P>
-  __device__ __forceinline__ void run_groups(const half4_t* ap, int gstride, int groups, float4_t (&acc)[P]) {
+  __device__ __forceinline__ void run_groups(const half8_t* ap, int gstride, int groups, float4_t (&acc)[P]) {
+    static_assert(NT % 2 == 0, "tile-row pairs");
 #pragma unroll
     for (int b = 0; b < NB; b++) {
       uint8_t* st = stage + (b & 1) * STAGE;
@@ -157,32 +132,29 @@ struct TileStream {
       if (b + 3 < NB) issue(b + 3);
       const uint32_t* tw = reinterpret_cast<const uint32_t*>(st);
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const half4_t bv = decode_group<K, CB>(tw[u * 8 * K + g.dw0], tw[u * 8 * K + g.dw1], g);
+      for (int v = 0; v < 4; v++) {
+        const uint32_t* t0 = tw + 2 * v * 8 * K;
+        const half8_t bv = decode_two_groups<K, CB>(t0[g.dw0], t0[g.dw1], t0[8 * K + g.dw0], t0[8 * K + g.dw1], g);
 #pragma unroll
         for (int p = 0; p < P; p++)
           if (p == 0 || p < groups)
-            acc[p] = __builtin_amdgcn_mfma_f32_16x16x16f16(ap[p * gstride + (b * 8 + u) * 4], bv, acc[p], 0, 0, 0);
+            acc[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ap[p * gstride + (b * 4 + v) * 4], bv, acc[p], 0, 0, 0);
       }
     }
   }
 };
 
-// A-operand staging in LDS: position p of the k-range, row m -> [m][p/16][q][e] with r = p % 16, q = (r & 7) >> 1,
-// e = (r & 1) | (r >> 3) << 1, rows mstride halves apart.  Lane (m, q) then reads its 4 activations for a tile as one
-// 8-byte word, in the row order 2q, 2q+1, 2q+8, 2q+9 the decoded group uses, at a 32-byte step per tile row;
-// mstride = 16 * tile rows + 4 keeps the 16 rows of a read in distinct banks.
+// A-operand staging in LDS, in the order of the tile-pair MFMAs: position p of the k-range (tile row u = p / 16,
+// r = p % 16), row m -> m * mstride + 32 (u / 2) + 8 q + 4 (u & 1) + e with q = (r & 7) >> 1,
+// e = (r & 1) | (r >> 3) << 1.  Lane (m, q) then reads its 8-half fragment [tile row 2v: rows 2q, 2q+1, 2q+8, 2q+9;
+// tile row 2v+1: the same rows] -- the row order of the decoded group -- as one 16-byte word, at a 64-byte step per
+// tile-row pair.  The order permutes positions inside each 32-position block only, so rows prepared in this order
+// (the rotation kernels that write prepared rows) are staged by plain copies.  mstride = 16 * tile rows + 8 keeps the
+// rows 16-byte aligned and the 16 rows of a read 16 bytes apart in the banks.
+__host__ __device__ constexpr int a_mstride(int NT) { return NT * 16 + 8; }
 __device__ __forceinline__ int a_slot(int p, int m, int mstride) {
-  const int r = p & 15;
-  return m * mstride + ((p >> 4) << 4) + (((r & 7) >> 1) << 2) + ((r & 1) | ((r >> 3) << 1));
-}
-
-// The same order with every value stored twice (a_slot_dup and a_slot_dup + 1): lane (m, q) reads its 8-half
-// fragment [a0, a0, a1, a1, a2, a2, a3, a3] for a tile as one 16-byte word, at a 64-byte step per tile row.
-// mstride = 32 * tile rows + 8 keeps the 16 rows of a read 16 bytes apart in the banks.
-__device__ __forceinline__ int a_slot_dup(int p, int m, int mstride) {
-  const int r = p & 15;
-  return m * mstride + ((p >> 4) << 5) + (((r & 7) >> 1) << 3) + (((r & 1) | ((r >> 3) << 1)) << 1);
+  const int r = p & 15, u = p >> 4;
+  return m * mstride + ((u >> 1) << 5) + (((r & 7) >> 1) << 3) + ((u & 1) << 2) + ((r & 1) | ((r >> 3) << 1));
 }
 
 }  // namespace exl3

@@ -246,8 +246,9 @@ def had_out_into(y: torch.Tensor, svh: torch.Tensor, out: torch.Tensor, col0: in
 
 def gemm_rotated(xh: torch.Tensor, trellis: torch.Tensor, codebook: int,
                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """xh @ W_inner in the rotated basis, fp32 accumulation, fp16 out; identity rows read W out exactly
-    (kernels/marlin.py:153-159)."""
+    """xh @ W_inner in the rotated basis, fp32 accumulation, fp16 out; identity rows read W_inner out exactly
+    (kernels/marlin.py:153-159).  Below 65 rows the decode-GEMV serves the rows, from 65 rows the prefill decode-GEMM,
+    as in a linear."""
     k, n, K = _check_trellis(trellis)
     xh = _half(xh, "xh")
     if xh.dim() != 2 or xh.shape[1] != k:
@@ -257,7 +258,7 @@ def gemm_rotated(xh: torch.Tensor, trellis: torch.Tensor, codebook: int,
         out = torch.empty((rows, n), dtype=torch.float16, device=xh.device)
     _check_out(out, (rows, n), xh, (torch.float16,))
     lib = _lib.load()
-    ws = workspace(xh.device, lib.exl3_linear_workspace_bytes(rows, k, n, K))
+    ws = workspace(xh.device, lib.exl3_gemm_rotated_workspace_bytes(rows, k, n, K))
     _lib.check(lib.exl3_gemm_rotated(xh.data_ptr(), rows, k, trellis.data_ptr(), n, K, int(codebook),
                                      out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(xh.device)), "gemm_rotated")
     return out
