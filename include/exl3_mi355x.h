@@ -171,6 +171,30 @@ int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const vo
                      int K_down, int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* One K class of a mixed-K MoE layer: the stacked weights of its experts in LOCAL order ([E_c][...] per tensor, as
+ * exl3_moe_weights), its bitrates, and its expert map (device int32 [num_experts]: global id -> local id, -1 for
+ * experts of other classes).  Replaces the per-class ExpertPack of the reference's MixedPack
+ * (cuda/src/sglang_exl3/kernels/marlin_moe.py:135-170). */
+typedef struct exl3_moe_class {
+  exl3_moe_weights weights;
+  const int* expert_map;
+  int num_local; /* E_c */
+  int K_gate_up, K_down;
+} exl3_moe_class;
+
+/* Workspace bytes of exl3_moe_forward_classes (the same layout as exl3_moe_forward's, with one k-split plan shared
+ * by the classes).  classes_host holds nclasses entries (only their bitrates are read). */
+size_t exl3_moe_classes_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter, int nclasses,
+                                        const exl3_moe_class* classes_host);
+/* exl3_moe_forward for a layer whose experts come in up to EXL3_MOE_MAX_CLASSES K classes; every expert id in
+ * [0, num_experts) must belong to exactly one class.  One routing for the layer, then each class's gate/up and down
+ * launches over its own experts (weights at their local ids), one combine.  The same results as exl3_moe_forward on
+ * a single class.  Replaces run_mixed (cuda/src/sglang_exl3/kernels/marlin_moe.py:247-272). */
+int exl3_moe_forward_classes(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids,
+                             const void* topk_weights, int top_k, int num_experts, int inter,
+                             const exl3_moe_class* classes_host, int nclasses, int codebook, void* y, int y_bf16,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- MoE per-launch stages (the reference's moe_align_decode, moe_had_in, moe_gemm, moe_glu_had_in, moe_combine:
  * cuda/csrc/exl3_marlin_moe.cu:376-618; run order cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294).  The same
  * arithmetic as exl3_moe_forward, one launch per stage, for callers that drive the stages themselves.  Weights are the
@@ -184,6 +208,19 @@ int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const vo
  * end), expert_ids max_blocks >= cap / block.  One workgroup; num_experts <= 1024. */
 int exl3_moe_align(const int* topk_ids, int slots, int num_experts, const int* expert_map, int block, int* sorted_ids,
                    int cap, int* expert_ids, int max_blocks, int* num_post_padded, void* stream);
+
+/* Mixed-K layers (e.g. 96 experts at K = 3 and 32 at K = 4): the routing of every class in ONE launch, for up to
+ * EXL3_MOE_MAX_CLASSES classes.  Class c gets the layout exl3_moe_align gives with expert_maps_host[c] (device int32
+ * [num_experts]: global id -> local id in the class, -1 for experts of other classes) and block size blocks_host[c],
+ * into sorted_ids_host[c] (caps_host[c] entries), expert_ids_host[c] (max_blocks_host[c] blocks, local ids) and
+ * *num_post_padded_host[c].  Every slot lands in the class its expert belongs to.  The *_host arrays hold nclasses
+ * entries each; the pointers in them are device memory.  Replaces moe_align_decode with two classes
+ * (cuda/csrc/exl3_marlin_moe.cu:532-618; caller cuda/src/sglang_exl3/kernels/marlin_moe.py:195-221). */
+#define EXL3_MOE_MAX_CLASSES 2
+int exl3_moe_align_classes(const int* topk_ids, int slots, int num_experts, int nclasses,
+                           const int* const* expert_maps_host, const int* blocks_host, int* const* sorted_ids_host,
+                           const int* caps_host, int* const* expert_ids_host, const int* max_blocks_host,
+                           int* const* num_post_padded_host, void* stream);
 
 /* xh[s * slots + slot][k] = fp16(Had(fp16(x[slot / top_k]) * suh_s[e])) (x fp16 or bf16 [tokens][k]) for every slot
  * with a valid expert e = topk_ids[slot] and every shard s < shards (1 or 2; suh: shards pointers to [E][k] fp16);

@@ -123,3 +123,29 @@ def test_reported_workspace_sizes_cover_every_launch_plan(lib):
                         (K, k, n, rows, lib.exl3_last_error())
                     assert lib.exl3_linear(P, 0, rows, k, arr, 1, K, 1, P, 0, P, need - 256, None) == \
                         _lib.EXL3_ERR_INVALID, (K, k, n, rows)
+
+
+def test_mixed_moe_entry_points_reject_bad_class_counts(lib):
+    P, I = ctypes.c_void_p, ctypes.c_int
+    maps, blocks = (P * 3)(1, 1, 1), (I * 3)(16, 16, 16)
+    outs, caps = (P * 3)(1, 1, 1), (I * 3)(1 << 20, 1 << 20, 1 << 20)
+    assert lib.exl3_moe_align_classes(1, 8, 16, 3, maps, blocks, outs, caps, outs, caps, outs, None) == \
+        _lib.EXL3_ERR_INVALID
+    assert "nclasses = 3" in lib.exl3_last_error().decode()
+    maps = (P * 2)(1, None)
+    assert lib.exl3_moe_align_classes(1, 8, 16, 2, maps, blocks, outs, caps, outs, caps, outs, None) == \
+        _lib.EXL3_ERR_INVALID
+    assert "expert map" in lib.exl3_last_error().decode()
+    cls = (_lib.Exl3MoeClass * 1)()
+    assert lib.exl3_moe_forward_classes(1, 0, 1, 256, 1, 1, 8, 16, 256, cls, 0, 1, 1, 0, 1, 1 << 20, None) == \
+        _lib.EXL3_ERR_INVALID
+    assert lib.exl3_moe_classes_workspace_bytes(4, 8, 16, 256, 256, 3, cls) == 0
+    cls = (_lib.Exl3MoeClass * 2)()
+    for c in range(2):
+        cls[c].weights = _lib.Exl3MoeWeights(*([1] * 9))
+        cls[c].num_local, cls[c].K_gate_up, cls[c].K_down = 8, 3, 4
+    cls[1].expert_map = 1
+    assert lib.exl3_moe_forward_classes(1, 0, 1, 256, 1, 1, 8, 16, 256, cls, 2, 1, 1, 0, 1, 1 << 20, None) == \
+        _lib.EXL3_ERR_INVALID
+    assert "no expert map" in lib.exl3_last_error().decode()
+    assert lib.exl3_moe_classes_workspace_bytes(4, 8, 16, 256, 256, 2, cls) > 0

@@ -119,6 +119,23 @@ def test_kv_decode_c5_32k_4bit_batch16():
     assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
 
 
+def test_kv_decode_c5_32k_8bit_batch16():
+    """The measured configuration at 32k context and 8-bit codes: B = 16, 40 / 8 heads, random page order."""
+    rng = np.random.default_rng(328)
+    lens = [32768] * 15 + [32768 - 3]
+    P = 16 * 2048
+    kc, vc = (rng.integers(-128, 128, size=(P, 8, PAGE, D), dtype=np.int8) for _ in range(2))
+    ks, vs = ((rng.random((P, 8)) * 0.01 + 0.004).astype(np.float16) for _ in range(2))
+    table = _table(rng, lens, 2048, P)
+    q = rng.standard_normal((16, 40, D)).astype(np.float16)
+    sm = D ** -0.5
+    y = _run(q, kc, vc, ks, vs, table, lens, 8, sm).cpu().numpy()
+    ref = orc.kv_decode_attention(q, kc, vc, ks, vs, table, np.asarray(lens, np.int32), 8, sm)
+    nrel, mrel = _errs(y, ref)
+    print(f"C5 32k 8-bit B=16: norm-rel {nrel:.2e} max-rel {mrel:.2e}")
+    assert nrel <= 2e-3 and mrel <= 2e-3, (nrel, mrel)
+
+
 @pytest.mark.parametrize("bits", [8, 4])
 def test_kv_decode_uniform_keys_give_mean_of_values(bits):
     """All-zero K codes: every logit is 0, so each head's output is the plain mean of its V rows (closed form)."""

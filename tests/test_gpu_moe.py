@@ -192,7 +192,8 @@ def test_moe_many_slots_use_the_routing_launch():
 def test_moe_full_shape_batched_tokens_match_single_token(coracle):
     """BASELINE configs[3] shape (128 experts, top-8, hidden 2048, inter 768, K = 3 MCG): every k-split plan covers
     all input rows.  One token against the exact layer (C reconstruct); batches of 16 and 256 tokens (other k-split
-    plans, other modes: only fp32 summation order differs) within 1e-3 of per-token calls."""
+    plans, other modes: only fp32 summation order differs) within 1e-3 of per-token calls, and sampled tokens of both
+    batches against the exact layer."""
     from conftest import c_reconstruct
     from trellis_serve_amd import ops
     rng = np.random.default_rng(48)
@@ -233,6 +234,21 @@ def test_moe_full_shape_batched_tokens_match_single_token(coracle):
         one = ops.moe_forward(x[t:t + 1], ids[t:t + 1], w[t:t + 1], st, cb).float()
         d = (y256[t] - one[0]).norm() / one[0].norm()
         assert d.item() <= 1e-3, (t, d.item())
+
+    # the batched calls themselves (the benchmark's T = 16 and T = 256 launches) against the exact layer on sampled
+    # tokens, each touched expert decoded by the C restatement
+    xs, ids_np, w_np = x.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()
+    for y, toks in ((y16, (3, 9, 15)), (y256, (0, 37, 81, 128, 199, 255))):
+        for t in toks:
+            for e in set(ids_np[t].tolist()):
+                if ex[e] is None:
+                    ex[e] = {p: tuple(st[f"{p}_{part}"][e].cpu().numpy() for part in ("trellis", "suh", "svh"))
+                             for p in ("gate", "up", "down")}
+                    for p in ("gate", "up", "down"):
+                        cache[(e, p)] = c_reconstruct(coracle, ex[e][p][0], K, cb)
+            ref = orc.moe_forward(xs[t:t + 1], ids_np[t:t + 1], w_np[t:t + 1], ex, K, cb, w_cache=cache)
+            nrel, mrel = _errs(y[t:t + 1].cpu().numpy(), ref)
+            assert nrel <= 2e-3 and mrel <= 2e-3, (y.shape[0], t, nrel, mrel)
 
 
 @pytest.mark.parametrize("T", [3, 20, 40, 300])

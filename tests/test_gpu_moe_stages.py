@@ -176,3 +176,89 @@ def test_combine_skips_unrouted_slots_and_rounds_once():
             if use[t, j]:
                 want[t] = want[t] + w[t, j] * yd[t * top_k + j].astype(np.float32)
     np.testing.assert_allclose(y.astype(np.float32), want.astype(np.float16).astype(np.float32), rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("block", [1, 16])
+def test_gemm_over_more_align_blocks_than_one_launch_counts(block):
+    """Every (align block, column block) of a launch has its own split counter in the 256 KiB counter region (65536
+    counters): 4096 slots in blocks of 1 over 32 column blocks need 131072, so the align blocks go out in two
+    launches (block 16: 4500 slots, 337 blocks, one launch).  Rows against fp32 matmuls of each expert's decoded weights
+    (no output transform), to the layer tolerance."""
+    rng = np.random.default_rng(900 + block)
+    E, k, n, K, cb = 8, 256, 4096, 2, 1
+    slots = 4096 if block == 1 else 4500
+    stack = torch.from_numpy(rng.integers(-32768, 32768, size=(E, k // 16, n // 16, 16 * K), dtype=np.int16)).cuda()
+    ids = torch.from_numpy(rng.integers(0, E, size=(slots, 1)).astype(np.int32)).cuda()
+    a = torch.from_numpy((rng.standard_normal((slots, k)) * 0.5).astype(np.float16)).cuda()
+    ops = _ops()
+    sorted_ids, expert_ids, post = ops.moe_align(ids, E, block)
+    assert expert_ids.numel() * n // 128 > 65536 or block == 16
+    c = ops.moe_gemm(a, [stack], None, sorted_ids, expert_ids, post, block, cb).float()
+    ref = torch.empty_like(c)
+    flat = ids.reshape(-1)
+    for e in range(E):
+        rows = (flat == e).nonzero().flatten()
+        ref[rows] = (a[rows].float() @ ops.reconstruct(stack[e], cb).float()).half().float()
+    d = (c - ref).norm() / ref.norm()
+    assert d.item() <= 2e-3, d.item()
+    assert ((c - ref).abs().max() / ref.abs().max()).item() <= 2e-3
+
+
+def test_stage_chain_replays_from_a_graph_after_reservation():
+    """The chained stages captured in one HIP graph after reserve_moe_stage (the library's workspaces do not grow in the
+    capture; every buffer is the caller's), and every replay, with eager work and synchronizations between replays,
+    equals the eager chain bit for bit."""
+    rng = np.random.default_rng(950)
+    E, H, I, K, top_k, T, block, cb = 16, 256, 384, 3, 4, 24, 16, 1
+    d = _stack(_experts(rng, E, H, I, K))
+    ops = _ops()
+    x = _dev((rng.standard_normal((T, H)) * 0.5).astype(np.float16))
+    it = _dev(_topk(rng, T, E, top_k))
+    logits = rng.standard_normal((T, top_k)).astype(np.float32)
+    wt = _dev((np.exp(logits) / np.exp(logits).sum(1, keepdims=True)).astype(np.float32))
+    slots = T * top_k
+    ops.reserve_moe_stage(x.device, slots, H, I, 2, E, block)
+    ops.reserve_moe_stage(x.device, slots, I, H, 1, E, block)
+    cap, max_blocks = ops.moe_align_capacity(slots, E, block)
+    st = dict(sorted=torch.empty(cap, dtype=torch.int32, device="cuda"),
+              eids=torch.empty(max_blocks, dtype=torch.int32, device="cuda"),
+              post=torch.empty(1, dtype=torch.int32, device="cuda"),
+              xh=torch.empty((2 * slots, H), dtype=torch.float16, device="cuda"),
+              gu=torch.empty((slots, 2 * I), dtype=torch.float16, device="cuda"),
+              act=torch.empty((slots, I), dtype=torch.float16, device="cuda"),
+              xd=torch.empty((slots, I), dtype=torch.float16, device="cuda"),
+              yd=torch.empty((slots, H), dtype=torch.float16, device="cuda"),
+              y=torch.empty((T, H), dtype=torch.float16, device="cuda"))
+    lib = ops._lib.load()
+
+    def chain():
+        ops._lib.check(lib.exl3_moe_align(it.data_ptr(), slots, E, None, block, st["sorted"].data_ptr(), cap,
+                                          st["eids"].data_ptr(), max_blocks, st["post"].data_ptr(),
+                                          ops._stream(x.device)), "moe_align")
+        ops.moe_had_in(x, [d["gate_suh"], d["up_suh"]], it, out=st["xh"])
+        ops.moe_gemm(st["xh"], [d["gate_trellis"], d["up_trellis"]], [d["gate_svh"], d["up_svh"]], st["sorted"],
+                     st["eids"], st["post"], block, cb, out=st["gu"])
+        ops.moe_glu_had_in(st["gu"], d["down_suh"], it, act=st["act"], out=st["xd"])
+        ops.moe_gemm(st["xd"], [d["down_trellis"]], [d["down_svh"]], st["sorted"], st["eids"], st["post"], block, cb,
+                     out=st["yd"])
+        ops.moe_combine(st["yd"], wt, it, E, out=st["y"])
+
+    chain()
+    torch.cuda.synchronize()
+    eager = st["y"].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        chain()   # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        chain()
+    for r in range(4):
+        st["y"].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(st["y"], eager), r
+        chain()   # eager work between replays
+        torch.cuda.synchronize()

@@ -16,6 +16,7 @@ HEADER = os.path.join(os.path.dirname(PKG), "include", "exl3_mi355x.h")
 
 EXL3_OK, EXL3_ERR_INVALID, EXL3_ERR_HIP, EXL3_ERR_UNSUPPORTED = 0, 1, 2, 3
 MAX_SHARDS = 4
+MAX_MOE_CLASSES = 2
 
 
 class ExtensionMissing(RuntimeError):
@@ -40,6 +41,11 @@ class Exl3MoeWeights(ctypes.Structure):
                                                       "gate_svh", "up_suh", "up_svh", "down_suh", "down_svh")]
 
 
+class Exl3MoeClass(ctypes.Structure):
+    _fields_ = [("weights", Exl3MoeWeights), ("expert_map", ctypes.c_void_p), ("num_local", ctypes.c_int),
+                ("K_gate_up", ctypes.c_int), ("K_down", ctypes.c_int)]
+
+
 _P, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 _SIGNATURES: dict[str, tuple] = {
     "exl3_abi_version": (_I, []),
@@ -61,7 +67,13 @@ _SIGNATURES: dict[str, tuple] = {
     "exl3_moe_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, _I]),
     "exl3_moe_forward": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, ctypes.POINTER(Exl3MoeWeights), _I, _I, _I, _P,
                               _I, _P, _SZ, _P]),
+    "exl3_moe_classes_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I, _I, ctypes.POINTER(Exl3MoeClass)]),
+    "exl3_moe_forward_classes": (_I, [_P, _I, _I, _I, _P, _P, _I, _I, _I, ctypes.POINTER(Exl3MoeClass), _I, _I, _P,
+                                      _I, _P, _SZ, _P]),
     "exl3_moe_align": (_I, [_P, _I, _I, _P, _I, _P, _I, _P, _I, _P, _P]),
+    "exl3_moe_align_classes": (_I, [_P, _I, _I, _I, ctypes.POINTER(_P), ctypes.POINTER(_I), ctypes.POINTER(_P),
+                                    ctypes.POINTER(_I), ctypes.POINTER(_P), ctypes.POINTER(_I), ctypes.POINTER(_P),
+                                    _P]),
     "exl3_moe_had_in": (_I, [_P, _I, _I, _I, _P, _I, _I, ctypes.POINTER(_P), _I, _P, _P]),
     "exl3_moe_gemm_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
     "exl3_moe_gemm": (_I, [_P, _I, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, _I, _P, _P, _P, _I, _I, _I, _I, _I,

@@ -57,7 +57,20 @@ struct MoeArgs {
   // [2][slots][H] (moe_route_prep_kernel) and down inputs [slots][I] (the gate/up reducer), both for several tokens
   const uint16_t* pre_in;
   const uint16_t* pre_dn;
+  // mixed-K layers: the launch serves one class, whose weights hold its experts at local ids (emap: global id ->
+  // local id, -1 for other classes' experts; null when one class holds every expert)
+  const int* emap;
+  int E_local;
 };
+
+// The weights' row of global expert e in the launch's class, or -1 when e is unrouted or belongs to another class.
+// Counters, routing lists and slot rows stay indexed by global ids and slots.
+__device__ __forceinline__ int moe_local(const MoeArgs& a, int e) {
+  if (e < 0 || e >= a.E) return -1;
+  if (a.emap == nullptr) return e;
+  const int el = a.emap[e];
+  return el < a.E_local ? el : -1;
+}
 
 
 // Activation buffers of the prepared-row chunk pipeline: two (chunk c + 1 staged while chunk c decodes) where the
@@ -171,15 +184,16 @@ __device__ void moe_route_block(const int* __restrict__ topk_ids, int slots, int
 
 constexpr int kMoePrepUnits = 4;  // 128-blocks per half-wave in moe_route_prep_kernel
 
-// moe_route_prep_kernel: workgroup 0 routes; workgroups 1 .. gridDim.x - 1 write the rotated gate/up inputs of every
-// routed slot, one half-wave per (slot, shard, 4 128-blocks) (rows of unrouted slots are left alone, never read).  One
-// launch for both: neither needs the other.
+// moe_route_prep_kernel: workgroup 0 routes (when `route`: the first class's launch of a mixed layer); workgroups
+// 1 .. gridDim.x - 1 write the rotated gate/up inputs of every routed slot of the launch's class, one half-wave per
+// (slot, shard, 4 128-blocks) (rows of unrouted slots are left alone, never read).  One launch for both: neither needs
+// the other.
 __global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const void* __restrict__ x, int x_bf16,
                                                              uint16_t* __restrict__ pre, int* __restrict__ counts,
                                                              int* __restrict__ n_active, int* __restrict__ active,
-                                                             int* __restrict__ lists) {
+                                                             int* __restrict__ lists, int route) {
   if (blockIdx.x == 0) {  // dispatched first: the routing chain is the longest at few tokens
-    moe_route_block(a.topk_ids, a.slots, a.E, counts, n_active, active, lists);
+    if (route) moe_route_block(a.topk_ids, a.slots, a.E, counts, n_active, active, lists);
     return;
   }
   // kMoePrepUnits consecutive 128-blocks of one (slot, shard) row per half-wave: their loads go out together and the
@@ -190,9 +204,9 @@ __global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const vo
   const int rest = u / groups, b0 = (u - rest * groups) * kMoePrepUnits;
   if (rest >= a.slots * 2) return;
   const int sh = rest & 1, slot = rest >> 1;
-  const int e = a.topk_ids[slot];
-  if (e < 0 || e >= a.E) return;
-  const uint16_t* suh = a.suh[sh] + (size_t)e * a.H;
+  const int el = moe_local(a, a.topk_ids[slot]);
+  if (el < 0) return;
+  const uint16_t* suh = a.suh[sh] + (size_t)el * a.H;
   _Float16* row = reinterpret_cast<_Float16*>(pre) + ((size_t)sh * a.slots + slot) * a.H;
   _Float16 h[kMoePrepUnits][4];
 #pragma unroll
@@ -224,22 +238,25 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
   // in one token are still right).  Slot mode is the launch without prepared rows (PRE = false), a compile-time
   // choice, so the single-token kernel has no routed-mode argument loads ahead of its expert id, and the empty asm
   // (taking the arguments as operands) puts every argument load into the round that fetches topk_ids.
-  int e, n_e, ctr_row;
+  int e, el, n_e, ctr_row;  // global expert id, its weights' row in this launch's class
   const int* list;
   if constexpr (!PRE)
     asm volatile("" ::"s"(a.tr[0]), "s"(a.tr[1]), "s"(a.tr[2]), "s"(a.suh[0]), "s"(a.suh[1]), "s"(a.suh[2]),
                  "s"(a.svh[0]), "s"(a.svh[1]), "s"(a.svh[2]), "s"(a.E), "s"(a.H), "s"(a.I), "s"(a.top_k),
                  "s"(a.topk_ids), "s"(x), "s"(x_bf16), "s"(gu), "s"(dn), "s"(partial), "s"(counters), "s"(splits),
-                 "s"(chunks));
+                 "s"(chunks), "s"(a.emap));
   if constexpr (!PRE) {
     e = a.topk_ids[blockIdx.y];
-    if (e < 0 || e >= a.E) return;
+    el = moe_local(a, e);
+    if (el < 0) return;
     n_e = 1;
     list = nullptr;
     ctr_row = blockIdx.y;
   } else {
     if ((int)blockIdx.y >= *a.n_active) return;
     e = a.active[blockIdx.y];
+    el = moe_local(a, e);
+    if (el < 0) return;
     n_e = a.counts[e];
     list = a.lists + (size_t)e * a.slots;
     ctr_row = e;
@@ -253,9 +270,9 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
   const int cbl = PHASE ? cb : cb - (sh ? a.I / 128 : 0);  // column block inside the shard
   const int tn = n_sh / 16;
   const int mat_bytes = (k >> 4) * tn * 32 * K;
-  const uint32_t* trellis = (sh == 0 ? a.tr[0] : sh == 1 ? a.tr[1] : a.tr[2]) + (size_t)e * (mat_bytes / 4);
-  const uint16_t* suh = (sh == 0 ? a.suh[0] : sh == 1 ? a.suh[1] : a.suh[2]) + (size_t)e * k;
-  const uint16_t* svh = (sh == 0 ? a.svh[0] : sh == 1 ? a.svh[1] : a.svh[2]) + (size_t)e * n_sh;
+  const uint32_t* trellis = (sh == 0 ? a.tr[0] : sh == 1 ? a.tr[1] : a.tr[2]) + (size_t)el * (mat_bytes / 4);
+  const uint16_t* suh = (sh == 0 ? a.suh[0] : sh == 1 ? a.suh[1] : a.suh[2]) + (size_t)el * k;
+  const uint16_t* svh = (sh == 0 ? a.svh[0] : sh == 1 ? a.svh[1] : a.svh[2]) + (size_t)el * n_sh;
   const uint16_t* pre = PRE ? (PHASE ? a.pre_dn : a.pre_in + (size_t)sh * a.slots * k) : nullptr;
   // this split's k range: `chunks` chunks of NB 128-row blocks, from chunk sp * chunks (the last split may hold fewer)
   const int kblocks = k >> 7;
@@ -437,9 +454,9 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
     // g and u of positions kk .. kk+3 of the intermediate, then a = fp16(silu(g) * u) * suh_down rotated: the down
     // inputs of those positions (exl3_marlin_moe.cu:228-258)
     const int kk = cbl * 128 + 4 * t;
-    const uint16_t* svg = a.svh[0] + (size_t)e * a.I + kk;
-    const uint16_t* svu = a.svh[1] + (size_t)e * a.I + kk;
-    const half4_t su = *reinterpret_cast<const half4_t*>(a.suh[2] + (size_t)e * a.I + kk);
+    const uint16_t* svg = a.svh[0] + (size_t)el * a.I + kk;
+    const uint16_t* svu = a.svh[1] + (size_t)el * a.I + kk;
+    const half4_t su = *reinterpret_cast<const half4_t*>(a.suh[2] + (size_t)el * a.I + kk);
     for (int m = hw; m < n_e; m += 2 * kMoeWaves) {
       const int slot = slot_at(m);
       _Float16 g[4], u[4];
@@ -620,54 +637,62 @@ static void launch_moe_gemv(const MoePlan& p, const MoePhase& ph, dim3 grid, con
   case KV * 4 + 1: { constexpr int kK = KV, kCB = 1; __VA_ARGS__; return true; }      \
   case KV * 4 + 2: { constexpr int kK = KV, kCB = 2; __VA_ARGS__; return true; }
 
-}  // namespace exl3
+// One K class of a layer as the launches take it: its weight stacks (local expert order), expert map and bitrates.
+struct MoeClass {
+  const exl3_moe_weights* w;
+  const int* emap;  // null: a single class holding every expert at its global id
+  int E_local, K_gu, K_dn;
+};
 
-using namespace exl3;
-
-extern "C" size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter,
-                                           int K_gate_up, int K_down) {
-  if (tokens <= 0 || top_k <= 0 || num_experts <= 0 || hidden <= 0 || inter <= 0) return 0;
-  if ((int64_t)num_experts * (2 * inter + hidden) / 128 > kMaxCounters) return 0;
-  return moe_plan(tokens, top_k, num_experts, hidden, inter, K_gate_up, K_down).total;
+// The classes share one plan: its k-splits come from the smallest bitrates (the partial-size cap is tightest there).
+static MoePlan moe_plan_of(int tokens, int top_k, int E, int H, int I, const MoeClass* cls, int ncls) {
+  int K_gu = cls[0].K_gu, K_dn = cls[0].K_dn;
+  for (int c = 1; c < ncls; c++) {
+    K_gu = std::min(K_gu, cls[c].K_gu);
+    K_dn = std::min(K_dn, cls[c].K_dn);
+  }
+  return moe_plan(tokens, top_k, E, H, I, K_gu, K_dn);
 }
 
-extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids,
-                                const void* topk_weights, int top_k, int num_experts, int inter,
-                                const exl3_moe_weights* w, int K_gate_up, int K_down, int codebook, void* y,
-                                int y_bf16, void* workspace, size_t workspace_bytes, void* stream) {
-  EXL3_CHECK_ARG(x && y && topk_ids && topk_weights && w, "exl3_moe_forward: null pointer");
-  EXL3_CHECK_ARG(valid_bits(K_gate_up) && valid_bits(K_down) && valid_cb(codebook),
-                 "exl3_moe_forward: K gate/up = %d, K down = %d, codebook = %d", K_gate_up, K_down, codebook);
-  EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= kMoeMaxTopK, "exl3_moe_forward: tokens = %d, top_k = %d",
-                 tokens, top_k);
-  EXL3_CHECK_ARG(num_experts >= 1 && num_experts <= 1024, "exl3_moe_forward: num_experts = %d (1..1024)", num_experts);
+static bool moe_shape_ok(int tokens, int top_k, int E, int H, int I) {
+  return tokens > 0 && top_k > 0 && E > 0 && H > 0 && I > 0 && (int64_t)E * (2 * I + H) / 128 <= kMaxCounters;
+}
+
+static int moe_forward_impl(const char* what, const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids,
+                            const void* topk_weights, int top_k, int num_experts, int inter, const MoeClass* cls,
+                            int ncls, int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes,
+                            hipStream_t st) {
+  EXL3_CHECK_ARG(x && y && topk_ids && topk_weights, "%s: null pointer", what);
+  EXL3_CHECK_ARG(valid_cb(codebook), "%s: codebook = %d", what, codebook);
+  EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= kMoeMaxTopK, "%s: tokens = %d, top_k = %d", what, tokens,
+                 top_k);
+  EXL3_CHECK_ARG(num_experts >= 1 && num_experts <= 1024, "%s: num_experts = %d (1..1024)", what, num_experts);
   EXL3_CHECK_ARG(hidden > 0 && hidden % 128 == 0 && inter > 0 && inter % 128 == 0,
-                 "exl3_moe_forward: hidden = %d, inter = %d (multiples of 128)", hidden, inter);
-  EXL3_CHECK_ARG(w->gate_trellis && w->up_trellis && w->down_trellis && w->gate_suh && w->gate_svh && w->up_suh &&
-                     w->up_svh && w->down_suh && w->down_svh,
-                 "exl3_moe_forward: null expert tensor");
-  EXL3_CHECK_ARG((int64_t)hidden * inter * std::max(K_gate_up, K_down) / 8 <= INT32_MAX,
-                 "exl3_moe_forward: expert matrix too large");
+                 "%s: hidden = %d, inter = %d (multiples of 128)", what, hidden, inter);
+  for (int c = 0; c < ncls; c++) {
+    const exl3_moe_weights* w = cls[c].w;
+    EXL3_CHECK_ARG(w && w->gate_trellis && w->up_trellis && w->down_trellis && w->gate_suh && w->gate_svh &&
+                       w->up_suh && w->up_svh && w->down_suh && w->down_svh,
+                   "%s: class %d: null expert tensor", what, c);
+    EXL3_CHECK_ARG(valid_bits(cls[c].K_gu) && valid_bits(cls[c].K_dn), "%s: class %d: K gate/up = %d, K down = %d",
+                   what, c, cls[c].K_gu, cls[c].K_dn);
+    EXL3_CHECK_ARG(cls[c].E_local >= 1 && cls[c].E_local <= num_experts, "%s: class %d holds %d experts of %d", what,
+                   c, cls[c].E_local, num_experts);
+    EXL3_CHECK_ARG(ncls == 1 || cls[c].emap, "%s: class %d of a mixed layer has no expert map", what, c);
+    EXL3_CHECK_ARG((int64_t)hidden * inter * std::max(cls[c].K_gu, cls[c].K_dn) / 8 <= INT32_MAX,
+                   "%s: expert matrix too large", what);
+  }
   EXL3_CHECK_ARG((int64_t)num_experts * (2 * inter + hidden) / 128 <= kMaxCounters,
-                 "exl3_moe_forward: %d experts x (2 x %d + %d) / 128 split counters exceed %d", num_experts, inter,
-                 hidden, kMaxCounters);
+                 "%s: %d experts x (2 x %d + %d) / 128 split counters exceed %d", what, num_experts, inter, hidden,
+                 kMaxCounters);
   if (tokens == 0) return EXL3_OK;
   const int slots = tokens * top_k;
-  EXL3_CHECK_ARG((int64_t)slots * std::max(2 * inter, hidden) <= INT32_MAX / 4, "exl3_moe_forward: too many slots");
-  const MoePlan p = moe_plan(tokens, top_k, num_experts, hidden, inter, K_gate_up, K_down);
-  EXL3_CHECK_ARG(workspace && workspace_bytes >= p.total, "exl3_moe_forward: workspace %zu bytes, need %zu",
-                 workspace_bytes, p.total);
+  EXL3_CHECK_ARG((int64_t)slots * std::max(2 * inter, hidden) <= INT32_MAX / 4, "%s: too many slots", what);
+  const MoePlan p = moe_plan_of(tokens, top_k, num_experts, hidden, inter, cls, ncls);
+  EXL3_CHECK_ARG(workspace && workspace_bytes >= p.total, "%s: workspace %zu bytes, need %zu", what, workspace_bytes,
+                 p.total);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   MoeArgs a{};
-  a.tr[0] = static_cast<const uint32_t*>(w->gate_trellis);
-  a.tr[1] = static_cast<const uint32_t*>(w->up_trellis);
-  a.tr[2] = static_cast<const uint32_t*>(w->down_trellis);
-  a.suh[0] = static_cast<const uint16_t*>(w->gate_suh);
-  a.suh[1] = static_cast<const uint16_t*>(w->up_suh);
-  a.suh[2] = static_cast<const uint16_t*>(w->down_suh);
-  a.svh[0] = static_cast<const uint16_t*>(w->gate_svh);
-  a.svh[1] = static_cast<const uint16_t*>(w->up_svh);
-  a.svh[2] = static_cast<const uint16_t*>(w->down_svh);
   a.E = num_experts;
   a.H = hidden;
   a.I = inter;
@@ -692,28 +717,54 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
   float* partial = reinterpret_cast<float*>(ws + p.off_partial);
   a.pre_in = pre_in;
   a.pre_dn = pre_dn;
-  hipStream_t st = as_stream(stream);
+  // the class's view of the arguments: its weight stacks and expert map
+  auto for_class = [&](int c) {
+    MoeArgs ac = a;
+    const exl3_moe_weights* w = cls[c].w;
+    ac.tr[0] = static_cast<const uint32_t*>(w->gate_trellis);
+    ac.tr[1] = static_cast<const uint32_t*>(w->up_trellis);
+    ac.tr[2] = static_cast<const uint32_t*>(w->down_trellis);
+    ac.suh[0] = static_cast<const uint16_t*>(w->gate_suh);
+    ac.suh[1] = static_cast<const uint16_t*>(w->up_suh);
+    ac.suh[2] = static_cast<const uint16_t*>(w->down_suh);
+    ac.svh[0] = static_cast<const uint16_t*>(w->gate_svh);
+    ac.svh[1] = static_cast<const uint16_t*>(w->up_svh);
+    ac.svh[2] = static_cast<const uint16_t*>(w->down_svh);
+    ac.emap = cls[c].emap;
+    ac.E_local = cls[c].E_local;
+    return ac;
+  };
 
-  if (!a.slot_mode) {
+  if (!a.slot_mode) {  // routing (once) and each class's rotated gate/up inputs
     const unsigned prep_wgs =
         (unsigned)(((size_t)slots * 2 * ((hidden / 128 + kMoePrepUnits - 1) / kMoePrepUnits) + 7) / 8);
-    moe_route_prep_kernel<<<prep_wgs + 1, 256, 0, st>>>(a, x, x_bf16, pre_in, counts, nactive, active, lists);
-    EXL3_CHECK_LAUNCH();
+    for (int c = 0; c < ncls; c++) {
+      moe_route_prep_kernel<<<prep_wgs + 1, 256, 0, st>>>(for_class(c), x, x_bf16, pre_in, counts, nactive, active,
+                                                           lists, c == 0);
+      EXL3_CHECK_LAUNCH();
+    }
   }
   const int rows = a.slot_mode ? slots : std::min(num_experts, slots);
+  // gate/up of every class (the GLU of each column block folded into its last arrival), then down of every class;
   // gate/up and down run at their own bitrates (a checkpoint may store down at another K than gate and up)
-  bool ok = EXL3_MOE_DISPATCH(K_gate_up, codebook, {
-    launch_moe_gemv<kK, kCB, 0>(p, p.gu, dim3(2 * inter / 128, rows), a, x, x_bf16, gu, pre_dn, dn, partial,
-                                cnt_gu, st);
-  });
-  if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_moe_forward: unsupported K/codebook");
-  EXL3_CHECK_LAUNCH();
-  ok = EXL3_MOE_DISPATCH(K_down, codebook, {
-    launch_moe_gemv<kK, kCB, 1>(p, p.dn, dim3(hidden / 128, rows), a, x, x_bf16, gu, pre_dn, dn, partial, cnt_dn,
-                                st);
-  });
-  if (!ok) return set_error(EXL3_ERR_INVALID, "exl3_moe_forward: unsupported K/codebook");
-  EXL3_CHECK_LAUNCH();
+  for (int c = 0; c < ncls; c++) {
+    const MoeArgs ac = for_class(c);
+    const bool ok = EXL3_MOE_DISPATCH(cls[c].K_gu, codebook, {
+      launch_moe_gemv<kK, kCB, 0>(p, p.gu, dim3(2 * inter / 128, rows), ac, x, x_bf16, gu, pre_dn, dn, partial,
+                                  cnt_gu, st);
+    });
+    if (!ok) return set_error(EXL3_ERR_INVALID, "%s: unsupported K/codebook", what);
+    EXL3_CHECK_LAUNCH();
+  }
+  for (int c = 0; c < ncls; c++) {
+    const MoeArgs ac = for_class(c);
+    const bool ok = EXL3_MOE_DISPATCH(cls[c].K_dn, codebook, {
+      launch_moe_gemv<kK, kCB, 1>(p, p.dn, dim3(hidden / 128, rows), ac, x, x_bf16, gu, pre_dn, dn, partial, cnt_dn,
+                                  st);
+    });
+    if (!ok) return set_error(EXL3_ERR_INVALID, "%s: unsupported K/codebook", what);
+    EXL3_CHECK_LAUNCH();
+  }
   const dim3 cgrid((unsigned)(((size_t)tokens * (hidden / 128) + 7) / 8));
   if (y_bf16)
     moe_combine_kernel<true><<<cgrid, 256, 0, st>>>(dn, static_cast<const int*>(topk_ids),
@@ -725,6 +776,52 @@ extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidde
                                                      num_experts, hidden, y);
   EXL3_CHECK_LAUNCH();
   return EXL3_OK;
+}
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" size_t exl3_moe_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter,
+                                           int K_gate_up, int K_down) {
+  if (!moe_shape_ok(tokens, top_k, num_experts, hidden, inter)) return 0;
+  return moe_plan(tokens, top_k, num_experts, hidden, inter, K_gate_up, K_down).total;
+}
+
+extern "C" size_t exl3_moe_classes_workspace_bytes(int tokens, int top_k, int num_experts, int hidden, int inter,
+                                                   int nclasses, const exl3_moe_class* classes_host) {
+  if (!moe_shape_ok(tokens, top_k, num_experts, hidden, inter) || !classes_host || nclasses < 1 ||
+      nclasses > EXL3_MOE_MAX_CLASSES)
+    return 0;
+  MoeClass cls[EXL3_MOE_MAX_CLASSES];
+  for (int c = 0; c < nclasses; c++)
+    cls[c] = MoeClass{nullptr, nullptr, 0, classes_host[c].K_gate_up, classes_host[c].K_down};
+  return moe_plan_of(tokens, top_k, num_experts, hidden, inter, cls, nclasses).total;
+}
+
+extern "C" int exl3_moe_forward(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids,
+                                const void* topk_weights, int top_k, int num_experts, int inter,
+                                const exl3_moe_weights* w, int K_gate_up, int K_down, int codebook, void* y,
+                                int y_bf16, void* workspace, size_t workspace_bytes, void* stream) {
+  const MoeClass one{w, nullptr, num_experts, K_gate_up, K_down};
+  return moe_forward_impl("exl3_moe_forward", x, x_bf16, tokens, hidden, topk_ids, topk_weights, top_k, num_experts,
+                          inter, &one, 1, codebook, y, y_bf16, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int exl3_moe_forward_classes(const void* x, int x_bf16, int tokens, int hidden, const void* topk_ids,
+                                        const void* topk_weights, int top_k, int num_experts, int inter,
+                                        const exl3_moe_class* classes_host, int nclasses, int codebook, void* y,
+                                        int y_bf16, void* workspace, size_t workspace_bytes, void* stream) {
+  EXL3_CHECK_ARG(classes_host && nclasses >= 1 && nclasses <= EXL3_MOE_MAX_CLASSES,
+                 "exl3_moe_forward_classes: nclasses = %d (1..%d)", nclasses, EXL3_MOE_MAX_CLASSES);
+  MoeClass cls[EXL3_MOE_MAX_CLASSES];
+  for (int c = 0; c < nclasses; c++) {
+    const exl3_moe_class& h = classes_host[c];
+    cls[c] = MoeClass{&h.weights, h.expert_map, h.num_local, h.K_gate_up, h.K_down};
+  }
+  return moe_forward_impl("exl3_moe_forward_classes", x, x_bf16, tokens, hidden, topk_ids, topk_weights, top_k,
+                          num_experts, inter, cls, nclasses, codebook, y, y_bf16, workspace, workspace_bytes,
+                          as_stream(stream));
 }
 
 extern "C" int exl3_moe_combine(const void* yd, const float* topk_weights, const int* topk_ids, int tokens, int top_k,

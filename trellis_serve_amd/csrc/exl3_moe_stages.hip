@@ -43,49 +43,62 @@ __host__ __device__ constexpr int stage_lds_bytes() {
   return 16 * P * kStageMStride * 2 + kStageWaves * stream_lds_bytes(K);
 }
 
-// ---- routing (one workgroup): per-expert counts (LDS atomics), padded runs by an exclusive scan, block experts, then
-// every slot into its expert's run.  Slots keep no particular order inside a run (rows of a block are independent).
+// ---- routing (one workgroup): per-expert counts (LDS atomics), then for each expert class (one class, or the K
+// classes of a mixed layer: each its own expert map and block size) the padded runs of its experts by an exclusive
+// scan, the block experts, and every slot of the class into its expert's run.  Slots keep no particular order inside
+// a run (rows of a block are independent).
+struct AlignClass {
+  const int* emap;  // global id -> local id, -1: not in this class; null: every id in [0, E), local = global
+  int block, cap, mblk;
+  int* sorted;
+  int* eids;
+  int* post;
+};
+struct AlignClasses {
+  AlignClass c[EXL3_MOE_MAX_CLASSES];
+  int n;
+};
+
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int* __restrict__ ids, int slots, int E,
-                                                                  const int* __restrict__ emap, int block,
-                                                                  int* __restrict__ sorted, int cap,
-                                                                  int* __restrict__ eids, int mblk,
-                                                                  int* __restrict__ post) {
+                                                                  AlignClasses ac) {
   __shared__ int cnt[kAlignMaxExperts], start[kAlignMaxExperts], fill[kAlignMaxExperts];
   __shared__ int scan[kAlignThreads];
   const int t = threadIdx.x;
-  for (int e = t; e < kAlignMaxExperts; e += kAlignThreads) {
-    cnt[e] = 0;
-    fill[e] = 0;
-  }
+  for (int e = t; e < kAlignMaxExperts; e += kAlignThreads) cnt[e] = 0;
   __syncthreads();
-  auto routed = [&](int e) { return e >= 0 && e < E && (emap == nullptr || emap[e] >= 0); };
   for (int s = t; s < slots; s += kAlignThreads) {
     const int e = ids[s];
-    if (routed(e)) atomicAdd(&cnt[e], 1);
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
   }
-  __syncthreads();
-  const int padded = t < E ? (cnt[t] + block - 1) / block * block : 0;
-  scan[t] = padded;
-  __syncthreads();
-  for (int d = 1; d < kAlignThreads; d <<= 1) {  // inclusive Hillis-Steele scan
-    const int v = t >= d ? scan[t - d] : 0;
+  for (int ci = 0; ci < ac.n; ci++) {
+    const AlignClass c = ac.c[ci];
+    for (int e = t; e < kAlignMaxExperts; e += kAlignThreads) fill[e] = 0;
+    __syncthreads();  // counts complete; the previous class's fills done
+    auto mine = [&](int e) { return e >= 0 && e < E && (c.emap == nullptr || c.emap[e] >= 0); };
+    const int padded = mine(t) ? (cnt[t] + c.block - 1) / c.block * c.block : 0;
+    scan[t] = padded;
     __syncthreads();
-    scan[t] += v;
+    for (int d = 1; d < kAlignThreads; d <<= 1) {  // inclusive Hillis-Steele scan
+      const int v = t >= d ? scan[t - d] : 0;
+      __syncthreads();
+      scan[t] += v;
+      __syncthreads();
+    }
+    const int total = scan[kAlignThreads - 1];
+    if (t < E) start[t] = scan[t] - padded;
+    // sentinels first (padding inside the runs and past the end), then the blocks' experts and the slots
+    for (int i = t; i < c.cap; i += kAlignThreads) c.sorted[i] = slots;
+    for (int i = t; i < c.mblk; i += kAlignThreads) c.eids[i] = -1;
     __syncthreads();
+    if (padded > 0)
+      for (int i = start[t]; i < start[t] + padded; i += c.block) c.eids[i / c.block] = c.emap ? c.emap[t] : t;
+    for (int s = t; s < slots; s += kAlignThreads) {
+      const int e = ids[s];
+      if (mine(e)) c.sorted[start[e] + atomicAdd(&fill[e], 1)] = s;
+    }
+    if (t == 0) *c.post = total;
+    __syncthreads();  // scan and start are rewritten by the next class
   }
-  const int total = scan[kAlignThreads - 1];
-  if (t < E) start[t] = scan[t] - padded;
-  // sentinels first (padding inside the runs and past the end), then the blocks' experts and the slots
-  for (int i = t; i < cap; i += kAlignThreads) sorted[i] = slots;
-  for (int i = t; i < mblk; i += kAlignThreads) eids[i] = -1;
-  __syncthreads();
-  if (t < E && padded > 0)
-    for (int i = start[t]; i < start[t] + padded; i += block) eids[i / block] = emap ? emap[t] : t;
-  for (int s = t; s < slots; s += kAlignThreads) {
-    const int e = ids[s];
-    if (routed(e)) sorted[start[e] + atomicAdd(&fill[e], 1)] = s;
-  }
-  if (t == 0) *post = total;
 }
 
 // ---- rotated expert inputs: one half-wave per (shard, slot, 128-block); rows of unrouted slots are left alone
@@ -294,22 +307,52 @@ static StagePlan stage_plan(int rows, int k, int n, int shards, int max_blocks) 
 
 using namespace exl3;
 
+static int check_align_class(const char* what, int slots, int num_experts, int block, int cap, int max_blocks,
+                             const int* sorted_ids, const int* expert_ids, const int* num_post_padded) {
+  EXL3_CHECK_ARG(sorted_ids && expert_ids && num_post_padded, "%s: null output pointer", what);
+  EXL3_CHECK_ARG(block >= 1 && block <= 64, "%s: block = %d (1..64)", what, block);
+  EXL3_CHECK_ARG((int64_t)cap >= (int64_t)slots + (int64_t)num_experts * (block - 1),
+                 "%s: sorted_ids holds %d entries, the padded runs may need %lld", what, cap,
+                 (long long)slots + (long long)num_experts * (block - 1));
+  EXL3_CHECK_ARG((int64_t)max_blocks * block >= cap, "%s: expert_ids holds %d blocks of %d, fewer than %d", what,
+                 max_blocks, block, cap);
+  return EXL3_OK;
+}
+
 extern "C" int exl3_moe_align(const int* topk_ids, int slots, int num_experts, const int* expert_map, int block,
                               int* sorted_ids, int cap, int* expert_ids, int max_blocks, int* num_post_padded,
                               void* stream) {
-  EXL3_CHECK_ARG(topk_ids && sorted_ids && expert_ids && num_post_padded, "exl3_moe_align: null pointer");
-  EXL3_CHECK_ARG(slots >= 0 && slots <= (1 << 24), "exl3_moe_align: slots = %d", slots);
-  EXL3_CHECK_ARG(num_experts >= 1 && num_experts <= kAlignMaxExperts, "exl3_moe_align: num_experts = %d (1..%d)",
+  return exl3_moe_align_classes(topk_ids, slots, num_experts, 1, &expert_map, &block, &sorted_ids, &cap, &expert_ids,
+                                &max_blocks, &num_post_padded, stream);
+}
+
+extern "C" int exl3_moe_align_classes(const int* topk_ids, int slots, int num_experts, int nclasses,
+                                      const int* const* expert_maps_host, const int* blocks_host,
+                                      int* const* sorted_ids_host, const int* caps_host,
+                                      int* const* expert_ids_host, const int* max_blocks_host,
+                                      int* const* num_post_padded_host, void* stream) {
+  const char* what = nclasses == 1 ? "exl3_moe_align" : "exl3_moe_align_classes";
+  EXL3_CHECK_ARG(topk_ids, "%s: null pointer", what);
+  EXL3_CHECK_ARG(nclasses >= 1 && nclasses <= EXL3_MOE_MAX_CLASSES, "%s: nclasses = %d (1..%d)", what, nclasses,
+                 EXL3_MOE_MAX_CLASSES);
+  EXL3_CHECK_ARG(expert_maps_host && blocks_host && sorted_ids_host && caps_host && expert_ids_host &&
+                     max_blocks_host && num_post_padded_host,
+                 "%s: null pointer", what);
+  EXL3_CHECK_ARG(slots >= 0 && slots <= (1 << 24), "%s: slots = %d", what, slots);
+  EXL3_CHECK_ARG(num_experts >= 1 && num_experts <= kAlignMaxExperts, "%s: num_experts = %d (1..%d)", what,
                  num_experts, kAlignMaxExperts);
-  EXL3_CHECK_ARG(block >= 1 && block <= 64, "exl3_moe_align: block = %d (1..64)", block);
-  EXL3_CHECK_ARG((int64_t)cap >= (int64_t)slots + (int64_t)num_experts * (block - 1),
-                 "exl3_moe_align: sorted_ids holds %d entries, the padded runs may need %lld", cap,
-                 (long long)slots + (long long)num_experts * (block - 1));
-  EXL3_CHECK_ARG((int64_t)max_blocks * block >= cap, "exl3_moe_align: expert_ids holds %d blocks of %d, fewer than %d",
-                 max_blocks, block, cap);
-  moe_align_kernel<<<1, kAlignThreads, 0, as_stream(stream)>>>(topk_ids, slots, num_experts, expert_map, block,
-                                                                 sorted_ids, cap, expert_ids, max_blocks,
-                                                                 num_post_padded);
+  EXL3_CHECK_ARG(nclasses == 1 || (expert_maps_host[0] && expert_maps_host[1]),
+                 "%s: every class of a mixed layer needs its expert map", what);
+  AlignClasses ac{};
+  ac.n = nclasses;
+  for (int c = 0; c < nclasses; c++) {
+    if (int rc = check_align_class(what, slots, num_experts, blocks_host[c], caps_host[c], max_blocks_host[c],
+                                   sorted_ids_host[c], expert_ids_host[c], num_post_padded_host[c]))
+      return rc;
+    ac.c[c] = AlignClass{expert_maps_host[c], blocks_host[c], caps_host[c], max_blocks_host[c], sorted_ids_host[c],
+                         expert_ids_host[c], num_post_padded_host[c]};
+  }
+  moe_align_kernel<<<1, kAlignThreads, 0, as_stream(stream)>>>(topk_ids, slots, num_experts, ac);
   EXL3_CHECK_LAUNCH();
   return EXL3_OK;
 }

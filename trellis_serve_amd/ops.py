@@ -152,6 +152,25 @@ def reserve_moe(device: torch.device, max_tokens: int, top_k: int, num_experts: 
     _ws("moe", dev).reserve(dev, need)
 
 
+def moe_align_capacity(slots: int, num_experts: int, block: int) -> tuple[int, int]:
+    """(sorted_ids entries, expert_ids blocks) that moe_align allocates for `slots` routed slots."""
+    cap = slots + num_experts * (block - 1)
+    return cap, -(-cap // block)
+
+
+def reserve_moe_stage(device: torch.device, max_slots: int, k: int, n: int, shards: int, num_experts: int,
+                      block: int) -> None:
+    """Reserves the grouped-GEMM workspace of the per-launch MoE stages (moe_gemm) for every call of up to `max_slots`
+    rows routed by moe_align with `num_experts` experts and this block size, so a captured stage chain never
+    allocates."""
+    lib = _lib.load()
+    dev = torch.device("cuda", _dev_index(device))
+    need = _max_need(lambda r: lib.exl3_moe_gemm_workspace_bytes(r, k, n, shards,
+                                                                 moe_align_capacity(r, num_experts, block)[1]),
+                     max_slots)
+    _ws("moe_stage", dev).reserve(dev, need)
+
+
 def reserve_kv(device: torch.device, max_batch: int, num_q_heads: int, num_kv_heads: int, max_pages: int) -> None:
     """Reserves the KV decode-attention workspace for batches of up to `max_batch` sequences of `max_pages` pages."""
     lib = _lib.load()
@@ -336,6 +355,37 @@ MOE_TENSORS = ("gate_trellis", "up_trellis", "down_trellis", "gate_suh", "gate_s
                "down_svh")
 
 
+def _expert_stacks(experts: dict[str, torch.Tensor], H: int, device: torch.device) -> tuple[int, int, int, int]:
+    """Checks one set of stacked expert tensors (MOE_TENSORS); returns (E, inter, K gate/up, K down)."""
+    gt, ut, dt = experts["gate_trellis"], experts["up_trellis"], experts["down_trellis"]
+    if any(t.dim() != 4 or t.dtype != torch.int16 for t in (gt, ut, dt)):
+        raise ValueError("stacked trellis tensors must be int16 [E, k/16, n/16, 16K]")
+    E, I = gt.shape[0], gt.shape[2] * 16
+    if ut.shape != gt.shape:
+        raise ValueError(f"gate {tuple(gt.shape)} and up {tuple(ut.shape)} must have one shape and bitrate")
+    if gt.shape[1] * 16 != H or tuple(dt.shape[:3]) != (E, I // 16, H // 16):
+        raise ValueError(f"expert shapes {tuple(gt.shape)} / {tuple(dt.shape)} do not match H = {H}")
+    sizes = {"gate_suh": H, "up_suh": H, "gate_svh": I, "up_svh": I, "down_suh": I, "down_svh": H}
+    for name in MOE_TENSORS:
+        t = experts[name]
+        if not (t.is_cuda and t.is_contiguous()) or t.shape[0] != E or t.device != device:
+            raise ValueError(f"{name} must be a contiguous tensor with {E} experts on {device}")
+        if name in sizes and (t.dtype != torch.float16 or tuple(t.shape) != (E, sizes[name])):
+            raise ValueError(f"{name} must be fp16 [{E}, {sizes[name]}], got {t.dtype} {tuple(t.shape)}")
+    return E, I, bits_of(gt), bits_of(dt)
+
+
+def _routing(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor):
+    T = x.shape[0]
+    if topk_ids.dim() != 2 or topk_ids.shape[0] != T or tuple(topk_weights.shape) != tuple(topk_ids.shape):
+        raise ValueError(f"topk_ids {tuple(topk_ids.shape)} and topk_weights {tuple(topk_weights.shape)} must both be "
+                         f"[{T}, top_k]")
+    if topk_ids.dtype not in (torch.int32, torch.int64) or topk_ids.device != x.device \
+            or topk_weights.device != x.device:
+        raise ValueError("topk_ids must be int32/int64 and both routing tensors on x's device")
+    return topk_ids.to(torch.int32).contiguous(), topk_weights.to(torch.float32).contiguous()
+
+
 def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor, experts: dict[str, torch.Tensor],
                 codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """Routed SiLU-gated EXL3 MoE layer (cuda/src/sglang_exl3/kernels/marlin_moe.py:272-294).
@@ -345,31 +395,9 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Ten
     if x.dtype not in (torch.float16, torch.bfloat16) or x.dim() != 2:
         raise ValueError("x must be a 2-D fp16/bf16 tensor")
     T, H = x.shape
-    gt, ut, dt = experts["gate_trellis"], experts["up_trellis"], experts["down_trellis"]
-    if any(t.dim() != 4 or t.dtype != torch.int16 for t in (gt, ut, dt)):
-        raise ValueError("stacked trellis tensors must be int16 [E, k/16, n/16, 16K]")
-    E, I = gt.shape[0], gt.shape[2] * 16
-    K_gu, K_dn = bits_of(gt), bits_of(dt)
-    if ut.shape != gt.shape:
-        raise ValueError(f"gate {tuple(gt.shape)} and up {tuple(ut.shape)} must have one shape and bitrate")
-    if gt.shape[1] * 16 != H or tuple(dt.shape[:3]) != (E, I // 16, H // 16):
-        raise ValueError(f"expert shapes {tuple(gt.shape)} / {tuple(dt.shape)} do not match H = {H}")
-    sizes = {"gate_suh": H, "up_suh": H, "gate_svh": I, "up_svh": I, "down_suh": I, "down_svh": H}
-    for name in MOE_TENSORS:
-        t = experts[name]
-        if not (t.is_cuda and t.is_contiguous()) or t.shape[0] != E or t.device != x.device:
-            raise ValueError(f"{name} must be a contiguous tensor with {E} experts on {x.device}")
-        if name in sizes and (t.dtype != torch.float16 or tuple(t.shape) != (E, sizes[name])):
-            raise ValueError(f"{name} must be fp16 [{E}, {sizes[name]}], got {t.dtype} {tuple(t.shape)}")
-    if topk_ids.dim() != 2 or topk_ids.shape[0] != T or tuple(topk_weights.shape) != tuple(topk_ids.shape):
-        raise ValueError(f"topk_ids {tuple(topk_ids.shape)} and topk_weights {tuple(topk_weights.shape)} must both be "
-                         f"[{T}, top_k]")
-    if topk_ids.dtype not in (torch.int32, torch.int64) or topk_ids.device != x.device \
-            or topk_weights.device != x.device:
-        raise ValueError("topk_ids must be int32/int64 and both routing tensors on x's device")
-    top_k = topk_ids.shape[1]
-    ids = topk_ids.to(torch.int32).contiguous()
-    w = topk_weights.to(torch.float32).contiguous()
+    E, I, K_gu, K_dn = _expert_stacks(experts, H, x.device)
+    ids, w = _routing(x, topk_ids, topk_weights)
+    top_k = ids.shape[1]
     if out is None:
         out = torch.empty((T, H), dtype=x.dtype, device=x.device)
     _check_out(out, (T, H), x)
@@ -381,6 +409,47 @@ def moe_forward(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Ten
                                     out.data_ptr(), int(out.dtype == torch.bfloat16), ws.data_ptr(), ws.numel(),
                                     _stream(x.device)),
                "moe_forward")
+    return out
+
+
+def moe_forward_classes(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                        classes: list[tuple[dict[str, torch.Tensor], torch.Tensor]], num_experts: int, codebook: int,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """moe_forward for a layer whose experts come in up to two K classes (the reference's MixedPack / run_mixed,
+    cuda/src/sglang_exl3/kernels/marlin_moe.py:135-170, 247-272): `classes` holds per class its stacked expert tensors
+    in LOCAL order and its expert map (int32 [num_experts]: global id -> local id, -1 for the other class's experts).
+    topk_ids hold global ids; every id in [0, num_experts) must belong to exactly one class."""
+    if x.dtype not in (torch.float16, torch.bfloat16) or x.dim() != 2:
+        raise ValueError("x must be a 2-D fp16/bf16 tensor")
+    if not 1 <= len(classes) <= _lib.MAX_MOE_CLASSES:
+        raise ValueError(f"1..{_lib.MAX_MOE_CLASSES} expert classes")
+    T, H = x.shape
+    arr = (_lib.Exl3MoeClass * len(classes))()
+    I0 = None
+    maps = []
+    for c, (experts, emap) in enumerate(classes):
+        E_c, I, K_gu, K_dn = _expert_stacks(experts, H, x.device)
+        if I0 is not None and I != I0:
+            raise ValueError("every class shares the intermediate width")
+        I0 = I
+        if emap.numel() != num_experts:
+            raise ValueError(f"class {c}: expert map holds {emap.numel()} entries for {num_experts} experts")
+        maps.append(_routing_ids(emap, x.device).reshape(-1))
+        arr[c] = _lib.Exl3MoeClass(_lib.Exl3MoeWeights(*[experts[n].data_ptr() for n in MOE_TENSORS]),
+                                   maps[-1].data_ptr(), E_c, K_gu, K_dn)
+    ids, w = _routing(x, topk_ids, topk_weights)
+    top_k = ids.shape[1]
+    if out is None:
+        out = torch.empty((T, H), dtype=x.dtype, device=x.device)
+    _check_out(out, (T, H), x)
+    lib = _lib.load()
+    ws = workspace(x.device, lib.exl3_moe_classes_workspace_bytes(T, top_k, num_experts, H, I0, len(classes), arr),
+                   "moe")
+    _lib.check(lib.exl3_moe_forward_classes(x.contiguous().data_ptr(), int(x.dtype == torch.bfloat16), T, H,
+                                            ids.data_ptr(), w.data_ptr(), top_k, num_experts, I0, arr, len(classes),
+                                            int(codebook), out.data_ptr(), int(out.dtype == torch.bfloat16),
+                                            ws.data_ptr(), ws.numel(), _stream(x.device)),
+               "moe_forward_classes")
     return out
 
 
@@ -404,8 +473,7 @@ def moe_align(topk_ids: torch.Tensor, num_experts: int, block: int, expert_map: 
     of `block` with the sentinel topk_ids.numel(), the expert (or expert_map[e]) of every block, -1 past the end."""
     ids = _routing_ids(topk_ids, topk_ids.device).reshape(-1)
     slots = ids.numel()
-    cap = slots + num_experts * (block - 1)
-    max_blocks = -(-cap // block)
+    cap, max_blocks = moe_align_capacity(slots, num_experts, block)
     dev = ids.device
     sorted_ids = torch.empty(cap, dtype=torch.int32, device=dev)
     expert_ids = torch.empty(max_blocks, dtype=torch.int32, device=dev)
@@ -419,6 +487,35 @@ def moe_align(topk_ids: torch.Tensor, num_experts: int, block: int, expert_map: 
                                           sorted_ids.data_ptr(), cap, expert_ids.data_ptr(), max_blocks,
                                           post.data_ptr(), _stream(dev)), "moe_align")
     return sorted_ids, expert_ids, post
+
+
+def moe_align_classes(topk_ids: torch.Tensor, num_experts: int, expert_maps: list[torch.Tensor],
+                      blocks: list[int]) -> list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
+    """moe_align for every K class of a mixed layer in one launch (the reference's moe_align_decode,
+    cuda/csrc/exl3_marlin_moe.cu:532-618): per class (sorted_ids, expert_ids, num_post_padded) as moe_align gives with
+    that class's expert map and block size (local expert ids)."""
+    n = len(expert_maps)
+    if not 1 <= n <= _lib.MAX_MOE_CLASSES or len(blocks) != n:
+        raise ValueError(f"1..{_lib.MAX_MOE_CLASSES} classes, one block size each")
+    ids = _routing_ids(topk_ids, topk_ids.device).reshape(-1)
+    slots, dev = ids.numel(), ids.device
+    maps = []
+    for emap in expert_maps:
+        if emap.numel() != num_experts:
+            raise ValueError(f"an expert map holds {emap.numel()} entries for {num_experts} experts")
+        maps.append(_routing_ids(emap, dev).reshape(-1))
+    out = []
+    for b in blocks:
+        cap, mb = moe_align_capacity(slots, num_experts, b)
+        out.append((torch.empty(cap, dtype=torch.int32, device=dev), torch.empty(mb, dtype=torch.int32, device=dev),
+                    torch.empty(1, dtype=torch.int32, device=dev)))
+    P, I = ctypes.c_void_p, ctypes.c_int
+    _lib.check(_lib.load().exl3_moe_align_classes(
+        ids.data_ptr(), slots, int(num_experts), n, (P * n)(*[m.data_ptr() for m in maps]), (I * n)(*blocks),
+        (P * n)(*[o[0].data_ptr() for o in out]), (I * n)(*[o[0].numel() for o in out]),
+        (P * n)(*[o[1].data_ptr() for o in out]), (I * n)(*[o[1].numel() for o in out]),
+        (P * n)(*[o[2].data_ptr() for o in out]), _stream(dev)), "moe_align_classes")
+    return out
 
 
 def moe_had_in(x: torch.Tensor, suh: list[torch.Tensor], topk_ids: torch.Tensor,
