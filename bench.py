@@ -557,12 +557,22 @@ def _under_profiler() -> bool:
 
 def probe(kind: str, launches: int) -> int:
     """Short GPU programs for counter passes: `gate_up` launches the dominant GEMV kernel `launches` times on one copy
-    of the layer; `copy` runs a plain 512 MiB device copy (the calibration of FETCH_SIZE / WRITE_SIZE)."""
+    of the layer; `prefill` the configs[2] decode-GEMM (5120 -> 17408, K = 3 MCG, M = 2048); `copy` runs a plain
+    512 MiB device copy (the calibration of FETCH_SIZE / WRITE_SIZE)."""
     import torch
 
     from trellis_serve_amd import ops
     dev = torch.device("cuda", 0)
-    if kind == "copy":
+    if kind == "prefill":
+        g = torch.Generator(device="cpu").manual_seed(5)
+        tr = torch.randint(-32768, 32768, (5120 // 16, 17408 // 16, 16 * K_BITS), dtype=torch.int16, generator=g).to(dev)
+        suh = (torch.randint(0, 2, (5120,), generator=g) * 2 - 1).half().to(dev)
+        svh = (torch.randint(0, 2, (17408,), generator=g) * 2 - 1).half().to(dev)
+        x = (torch.randn((2048, 5120), generator=g) * 0.5).half().to(dev)
+        y = ops.linear_prefill(x, [tr], [suh], [svh], CODEBOOK)
+        for _ in range(launches):
+            ops.linear_prefill(x, [tr], [suh], [svh], CODEBOOK, out=y)
+    elif kind == "copy":
         src = torch.empty(128 << 20, dtype=torch.float32, device=dev).uniform_()
         dst = torch.empty_like(src)
         for _ in range(3):
@@ -627,7 +637,7 @@ def main() -> int:
                     help="also report these M (comma list, '' for none; past 16 rows the GEMV takes 2 or 4 row groups)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-secondary", action="store_true", help="skip the prefill / MoE / KV-attention lines")
-    ap.add_argument("--probe", choices=["gate_up", "copy"], help=argparse.SUPPRESS)
+    ap.add_argument("--probe", choices=["gate_up", "prefill", "copy"], help=argparse.SUPPRESS)
     ap.add_argument("--probe-launches", type=int, default=20, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.probe:
