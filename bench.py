@@ -52,10 +52,12 @@ def alg_bytes(k: int, ns: list[int], M: int, K: int) -> int:
     return k * n * K // 8 + 2 * k * len(ns) + 2 * n + 2 * M * k + 2 * M * n
 
 
-def make_layer_set(torch, rng_seed: int, device):
+def make_layer_set(torch, rng_seed: int, device, names=None):
     g = torch.Generator(device="cpu").manual_seed(rng_seed)
     out = {}
     for name, (k, ns) in LAYERS.items():
+        if names is not None and name not in names:
+            continue
         trs, suhs, svhs = [], [], []
         for n in ns:
             t = torch.randint(-32768, 32768, (k // 16, n // 16, 16 * K_BITS), dtype=torch.int16, generator=g)
@@ -341,11 +343,17 @@ DOMINANT = "gate_up"  # the largest fused linear: its gemv_kernel instance is th
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
 
-def _graph_us(torch, fn, calls: int, reps: int = 3) -> float:
-    """Mean device time of fn() in microseconds: a graph of `calls` back-to-back calls, replayed `reps` times."""
+def _graph_us(torch, fn, calls: int, reps: int = 3, warm_s: float = 0.05) -> float:
+    """Mean device time of fn() in microseconds: a graph of `calls` back-to-back calls, replayed `reps` times after
+    untimed replays for at least `warm_s` seconds (the inputs of each secondary line are generated on the host first,
+    which leaves the GPU idle long enough for its clock to drop: one warm replay read the prefill ~7 % slow)."""
     g = _capture(torch, lambda: [fn(i) for i in range(calls)])
+    t_end = time.perf_counter() + warm_s
     g.replay()
     torch.cuda.synchronize()
+    while time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -556,8 +564,8 @@ def _under_profiler() -> bool:
 
 
 def probe(kind: str, launches: int) -> int:
-    """Short GPU programs for counter passes: `gate_up` launches the dominant GEMV kernel `launches` times on one copy
-    of the layer; `prefill` the configs[2] decode-GEMM (5120 -> 17408, K = 3 MCG, M = 2048); `copy` runs a plain
+    """Short GPU programs for counter passes: `gate_up` launches the dominant GEMV kernel `launches` times over five
+    rotating copies of the layer; `prefill` the configs[2] decode-GEMM (5120 -> 17408, K = 3 MCG, M = 2048); `copy` runs a plain
     512 MiB device copy (the calibration of FETCH_SIZE / WRITE_SIZE)."""
     import torch
 
@@ -578,12 +586,14 @@ def probe(kind: str, launches: int) -> int:
         for _ in range(3):
             dst.copy_(src)
     else:
+        # five copies of the layer (5 x 67 MB > the 256 MB MALL), rotated as the timed step rotates its copies, so the
+        # counters see weights coming from HBM rather than from the MALL
         k, ns = LAYERS[kind]
-        s = make_layer_set(torch, 99, dev)[kind]
+        copies = [make_layer_set(torch, 99 + r, dev, names=(kind,))[kind] for r in range(5)]
         x = torch.randn((1, k), dtype=torch.float16, device=dev)
-        out = ops.linear(x, *s, CODEBOOK)
-        for _ in range(launches):
-            ops.linear(x, *s, CODEBOOK, out=out)
+        out = ops.linear(x, *copies[0], CODEBOOK)
+        for i in range(launches):
+            ops.linear(x, *copies[i % len(copies)], CODEBOOK, out=out)
     torch.cuda.synchronize()
     return 0
 
