@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 5
+#define EXL3_ABI_VERSION 6
 
 enum {
   EXL3_OK = 0,
@@ -45,11 +45,20 @@ enum {
  * of y in order.  Replaces the per-shard tensors of exl3_linear_marlin_multi_out (cuda/csrc/exl3_marlin.cu:507-527)
  * and the shard map of the Marlin template (exl3_marlin_template.h:298-302, 605-610). */
 typedef struct exl3_shard {
-  const void* trellis; /* int16 [k/16, n/16, 16K] */
+  const void* trellis; /* the trellis in `layout`: the stored int16 [k/16, n/16, 16K], or exl3_repack_trellis's */
   const void* suh;     /* fp16 [k] */
   const void* svh;     /* fp16 [n] */
   int n;               /* output columns of this shard (multiple of 128) */
+  int layout;          /* EXL3_LAYOUT_STORED (0, zero-initialised callers) or EXL3_LAYOUT_BLOCKS */
 } exl3_shard;
+
+/* Trellis layouts.  STORED: the checkpoint's int16 [k/16, n/16, 16K], tile (i, j) at byte (i n/16 + j) 32K.
+ * BLOCKS: the load-time layout of exl3_repack_trellis, the same tiles reordered so that each (128-column block cb,
+ * 128-row block kb) unit of 8 x 8 tiles is one contiguous 2048K-byte run, units column block major, and inside a
+ * unit the 8 tiles of each tile column contiguous: tile (i, j) at byte
+ * ((j / 8) (k / 128) + i / 8) 2048K + ((j % 8) 8 + i % 8) 32K.  Same bytes per tile, lossless. */
+#define EXL3_LAYOUT_STORED 0
+#define EXL3_LAYOUT_BLOCKS 1
 
 /* ---- process / device ---------------------------------------------------------------------------------------- */
 int exl3_abi_version(void);

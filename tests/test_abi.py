@@ -23,7 +23,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_abi_version(lib):
-    assert lib.exl3_abi_version() == 5
+    assert lib.exl3_abi_version() == 6
 
 
 def test_workspace_size_is_deterministic_and_zero_for_bad_shapes(lib):
@@ -85,6 +85,17 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
 
 def test_shard_struct_layout():
     assert ctypes.sizeof(_lib.Exl3Shard) == 32
+    assert _lib.Exl3Shard.layout.offset == 28   # in the padding after n: zero-initialised callers get STORED
+
+
+def test_unknown_layout_and_aliased_repack_are_rejected_without_launching(lib):
+    arr = (_lib.Exl3Shard * 1)(_lib.Exl3Shard(1, 1, 1, 128, 2))
+    assert lib.exl3_linear(1, 0, 1, 128, arr, 1, 3, 1, 1, 0, 1, 1 << 20, None) == _lib.EXL3_ERR_INVALID
+    assert "layout" in lib.exl3_last_error().decode()
+    assert lib.exl3_linear_prefill(1, 0, 1, 128, arr, 1, 3, 1, 1, 0, 1, 1 << 30, None) == _lib.EXL3_ERR_INVALID
+    assert "layout" in lib.exl3_last_error().decode()
+    assert lib.exl3_repack_trellis(16, 128, 128, 3, 16, None) == _lib.EXL3_ERR_INVALID   # out aliases the input
+    assert lib.exl3_unpack_trellis(16, 128, 64, 3, 32, None) == _lib.EXL3_ERR_INVALID    # n not a multiple of 128
 
 
 def test_noalloc_rejects_calls_beyond_the_scratch(lib):

@@ -36,6 +36,14 @@ def _dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+def blocks_layout(tr):
+    """The EXL3_LAYOUT_BLOCKS order of a stored trellis [k/16, n/16, 16K] (include/exl3_mi355x.h): tile (i, j) at tile
+    position ((j / 8) (k / 128) + i / 8) 64 + (j % 8) 8 + i % 8, returned in the stored array's shape."""
+    tk, tn, w = tr.shape
+    units = tr.reshape(tk // 8, 8, tn // 8, 8, w)           # [kb][i%8][cb][j%8][w]
+    return np.ascontiguousarray(units.transpose(2, 0, 3, 1, 4)).reshape(tk, tn, w)  # [cb][kb][j%8][i%8][w]
+
+
 def _errs(y, ref):
     y = y.astype(np.float64)
     ref = ref.astype(np.float64)
@@ -200,20 +208,25 @@ def test_row_counts_either_side_of_the_row_group_switch_agree(coracle):
 
 @pytest.mark.parametrize("K", KS)
 def test_repack_is_lossless_and_the_kernels_read_it(coracle, K):
-    """repack -> unpack returns the stored trellis bit for bit (the invertibility check of
-    cuda/src/sglang_exl3/parity/marlin_parity.py:173), in place as well, and the repacked form decodes to the
-    oracle's weights."""
+    """repack writes the BLOCKS layout (each (128-column block, 128-row block) unit of 64 tiles one run, the 8 tiles of
+    a tile column adjacent inside it) bit for bit as blocks_layout restates it; unpack returns the stored trellis bit
+    for bit (the invertibility check of cuda/src/sglang_exl3/parity/marlin_parity.py:173); an in-place repack is
+    refused; and the GEMV and the prefill decode-GEMM read the repacked form to the same bits as the stored one."""
     rng = np.random.default_rng(500 + K)
     tr = _trellis(rng, 256, 384, K)
     t = torch.from_numpy(tr).cuda()
     ops = _ops()
     packed = ops.repack_trellis(t)
-    assert packed.data_ptr() != t.data_ptr()
+    np.testing.assert_array_equal(packed.cpu().numpy(), blocks_layout(tr))
     np.testing.assert_array_equal(ops.unpack_trellis(packed).cpu().numpy(), tr)
-    assert ops.repack_trellis(t, out=t).data_ptr() == t.data_ptr()
-    np.testing.assert_array_equal(t.cpu().numpy(), tr)
-    w = ops.reconstruct(packed, 1).cpu().numpy()
-    np.testing.assert_array_equal(w.view(np.uint16), c_reconstruct(coracle, tr, K, 1).view(np.uint16))
+    with pytest.raises(ValueError):
+        ops.repack_trellis(t, out=t)
+    su, sv = _dev(_signs(rng, 256)), _dev(_signs(rng, 384))
+    for rows, fn in ((1, ops.linear), (5, ops.linear), (40, ops.linear), (300, ops.linear_prefill)):
+        x = _dev(rng.standard_normal((rows, 256)).astype(np.float16))
+        y0 = fn(x, [t], [su], [sv], 1)
+        y1 = fn(x, [packed], [su], [sv], 1, layout=1)
+        assert torch.equal(y0, y1), (rows, fn.__name__)
 
 
 @pytest.mark.parametrize("K", (2, 3, 4))
@@ -331,6 +344,29 @@ def test_linear_fused_group_matches_oracle_per_shard(coracle):
         nrel, mrel = _errs(y[:, col:col + n], ref)
         assert nrel <= TOL and mrel <= TOL, (n, nrel, mrel)
         col += n
+
+
+@pytest.mark.parametrize("K", KS)
+@pytest.mark.parametrize("cb", CBS)
+def test_repacked_group_matches_oracle(coracle, K, cb):
+    """A 3-shard group in the repacked (BLOCKS) layout, each shard a different number of 128-column blocks, through
+    the decode-GEMV (1 and 16 rows) and the prefill decode-GEMM (80 rows), against the float64 oracle of the stored
+    trellis."""
+    rng = np.random.default_rng(900 + 10 * K + cb)
+    k, ns = 384, (256, 128, 384)
+    trs = [_trellis(rng, k, n, K) for n in ns]
+    suhs, svhs = [_signs(rng, k) for _ in ns], [_signs(rng, n) for n in ns]
+    ops = _ops()
+    packed = [ops.repack_trellis(_dev(t)) for t in trs]
+    for rows, fn in ((1, ops.linear), (16, ops.linear), (80, ops.linear_prefill)):
+        x = rng.standard_normal((rows, k)).astype(np.float16)
+        y = fn(_dev(x), packed, [_dev(v) for v in suhs], [_dev(v) for v in svhs], cb, layout=1).cpu().numpy()
+        col = 0
+        for t, su, sv, n in zip(trs, suhs, svhs, ns):
+            ref = orc.linear_forward(x, t, su, sv, K, cb, w_inner=c_reconstruct(coracle, t, K, cb), dtype=np.float64)
+            nrel, mrel = _errs(y[:, col:col + n], ref)
+            assert nrel <= TOL and mrel <= TOL, (rows, n, nrel, mrel)
+            col += n
 
 
 def test_linear_is_deterministic():

@@ -60,6 +60,19 @@ def test_gemv_c2_layer_set_shapes(name, M):
     _check(_ops().linear(x, trs, suhs, svhs, 1), _reference(x, trs, suhs, svhs, 1))
 
 
+@pytest.mark.parametrize("name", list(C2_LAYERS))
+def test_c2_layer_set_shapes_read_the_repacked_layout_bit_identically(name):
+    """configs[1] at M = 1 with the trellis repacked to the BLOCKS layout: the decode-GEMV gives the same bits as on
+    the stored layout (the split-K chain runs in one XCD's L2 here: every layer has a multiple of 8 column blocks)."""
+    g = torch.Generator(device="cpu").manual_seed(7)
+    k, ns = C2_LAYERS[name]
+    trs, suhs, svhs = _layer(g, k, ns, 3)
+    ops = _ops()
+    packed = [ops.repack_trellis(t) for t in trs]
+    x = torch.randn((1, k), generator=g).half().cuda()
+    assert torch.equal(ops.linear(x, trs, suhs, svhs, 1), ops.linear(x, packed, suhs, svhs, 1, layout=1))
+
+
 @pytest.mark.parametrize("K,cb,M", [(3, 1, 2048), (2, 0, 512), (8, 2, 512), (3, 1, 8192), (4, 2, 2048), (5, 1, 2048),
                                     (6, 0, 2048), (2, 0, 2048), (8, 2, 2048)])
 def test_prefill_c3_shape(K, cb, M):

@@ -31,9 +31,12 @@ class Exl3Error(RuntimeError):
         self.code = code
 
 
+LAYOUT_STORED, LAYOUT_BLOCKS = 0, 1
+
+
 class Exl3Shard(ctypes.Structure):
     _fields_ = [("trellis", ctypes.c_void_p), ("suh", ctypes.c_void_p), ("svh", ctypes.c_void_p),
-                ("n", ctypes.c_int)]
+                ("n", ctypes.c_int), ("layout", ctypes.c_int)]
 
 
 class Exl3MoeWeights(ctypes.Structure):

@@ -42,6 +42,10 @@ size_t prefill_plain_workspace_bytes(int rows, int k, int n);
 int prefill_plain_gemm(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook, void* out,
                        void* workspace, size_t workspace_bytes, hipStream_t st);
 
+// exl3_init_device's probe of the workgroup -> XCD assignment (exl3_linear.hip): enables split-K chains that stay
+// in one XCD's L2
+int xcd_probe(int device);
+
 inline bool valid_bits(int K) { return K == 2 || K == 3 || K == 4 || K == 5 || K == 6 || K == 8; }
 inline bool valid_cb(int cb) { return cb >= 0 && cb <= 2; }
 

@@ -67,6 +67,7 @@ struct GemmShards {
   const uint16_t* svh[EXL3_MAX_SHARDS];
   const uint16_t* xh[EXL3_MAX_SHARDS];  // per-shard rotated activations, fragment order, k-step major
   int tn[EXL3_MAX_SHARDS];              // tile columns of the shard
+  int layout[EXL3_MAX_SHARDS];          // EXL3_LAYOUT_STORED / EXL3_LAYOUT_BLOCKS
   int col0[EXL3_MAX_SHARDS];            // first output column of the shard
   int ct0[EXL3_MAX_SHARDS + 1];         // first 256-column tile of the shard (cumulative); ct0[count] = total
   int count;
@@ -306,7 +307,13 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
   const int row_bytes = tn * tile_bytes;
   const __amdgpu_buffer_rsrc_t brsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)sa.trellis[s], (short)0, (k >> 4) * row_bytes, 0x00020000);
-  const int bgoff = (tc0 + (btc < ntc ? btc : 0)) * tile_bytes + min(l, CHUNKS - 1) * 16;  // + tile row * row_bytes
+  // STORED: the 4 tiles are adjacent in their tile row (+ tile row * row_bytes); BLOCKS: 8 tiles apart inside the
+  // unit of the column block (+ the unit of the 128-row block and the row inside it, per k-step)
+  const bool blocks = sa.layout[s] == EXL3_LAYOUT_BLOCKS;
+  const int bj0 = tc0 + (btc < ntc ? btc : 0), bL = min(l, CHUNKS - 1);
+  const int bgoff = blocks ? ((bj0 >> 3) * (k >> 7) * 64 + ((bj0 & 7) + bL / (2 * K)) * 8) * tile_bytes +
+                                 (bL % (2 * K)) * 16
+                           : bj0 * tile_bytes + bL * 16;
   const LaneGeo g = lane_geo<K>(c, j);
 
   // A: wave w loads m-blocks 2w, 2w+1; lane l of a piece = row (l % 16) of the m-block, k-chunk l / 16.  Rows past
@@ -336,8 +343,10 @@ __device__ __forceinline__ void gemm_segment(const GemmShards& sa, const GemmPla
   };
   auto issue_bits = [&](int i, int kt) {
     uint8_t* st = bits_ring + (i % kRing) * kBitsStage + w * 1024;
+    const int tr = 2 * kt + btr;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, (__attribute__((address_space(3))) void*)st, 16, bgoff,
-                                             (2 * kt + btr) * row_bytes, 0, 0);
+                                             blocks ? ((tr >> 3) * 64 + (tr & 7)) * tile_bytes : tr * row_bytes, 0,
+                                             0);
   };
   // this wave's trellis words of step i (bits slot i % 3)
   auto read_bits = [&](int i, uint32_t (&bw)[4][2]) {
@@ -738,6 +747,9 @@ extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, c
     sa.svh[s] = static_cast<const uint16_t*>(sh.svh);
     su.suh[s] = static_cast<const uint16_t*>(sh.suh);
     sa.tn[s] = sh.n / 16;
+    EXL3_CHECK_ARG(sh.layout == EXL3_LAYOUT_STORED || sh.layout == EXL3_LAYOUT_BLOCKS, "shard %d: layout %d", s,
+                   sh.layout);
+    sa.layout[s] = sh.layout;
     sa.col0[s] = col;
     sa.ct0[s] = ctl;
     shard_n[s] = sh.n;

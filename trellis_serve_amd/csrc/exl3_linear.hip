@@ -11,7 +11,9 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
+#include <vector>
 
 #include "exl3_api.hpp"
 #include "exl3_device.hpp"
@@ -30,6 +32,7 @@ struct ShardArgs {
   const uint16_t* suh[EXL3_MAX_SHARDS];
   const uint16_t* svh[EXL3_MAX_SHARDS];
   int tn[EXL3_MAX_SHARDS];            // tile columns (n / 16)
+  int layout[EXL3_MAX_SHARDS];        // EXL3_LAYOUT_STORED / EXL3_LAYOUT_BLOCKS
   int col0[EXL3_MAX_SHARDS];          // first output column
   int blk0[EXL3_MAX_SHARDS + 1];      // first 128-column block (cumulative); blk0[count] = total blocks
   int count;
@@ -43,7 +46,7 @@ struct ShardView {
   const uint32_t* trellis;
   const uint16_t* suh;
   const uint16_t* svh;
-  int tn, col0, blk0;
+  int tn, col0, blk0, layout;
 };
 
 // Every field of every shard is read into scalar registers before the compares (the empty asm statements take them
@@ -53,8 +56,9 @@ __device__ __forceinline__ ShardView shard_of_block(const ShardArgs& sa, int blk
   ShardView f[EXL3_MAX_SHARDS];
 #pragma unroll
   for (int i = 0; i < EXL3_MAX_SHARDS; i++) {
-    f[i] = ShardView{sa.trellis[i], sa.suh[i], sa.svh[i], sa.tn[i], sa.col0[i], sa.blk0[i]};
-    asm volatile("" ::"s"(f[i].trellis), "s"(f[i].suh), "s"(f[i].svh), "s"(f[i].tn), "s"(f[i].col0), "s"(f[i].blk0));
+    f[i] = ShardView{sa.trellis[i], sa.suh[i], sa.svh[i], sa.tn[i], sa.col0[i], sa.blk0[i], sa.layout[i]};
+    asm volatile("" ::"s"(f[i].trellis), "s"(f[i].suh), "s"(f[i].svh), "s"(f[i].tn), "s"(f[i].col0), "s"(f[i].blk0),
+                 "s"(f[i].layout));
   }
   const int count = sa.count;
   asm volatile("" ::"s"(count));
@@ -219,6 +223,7 @@ __global__ __launch_bounds__(256) void had_out_kernel(const uint16_t* __restrict
 // stores y, then resets the counter to zero for the next call.
 constexpr int kGemvThreads = kGemvWaves * 64;
 constexpr int kCoherentDevice = 1 << 4;  // buffer cache policy sc1: device-scope coherent access
+constexpr int kBypassL1 = 1;             // buffer cache policy sc0: miss the L1, read the L2
 constexpr int kWaitVmcnt0 = 0x0F70;      // s_waitcnt vmcnt(0) (expcnt, lgkmcnt unconstrained)
 
 // LDS bytes of the GEMV: staged activations (M rows of a_mstride(NT) halves), then per wave two block stages of 256*K
@@ -240,9 +245,14 @@ template <int K, int CB, bool ROTATE, int NT, bool PRE = false, int P = 1>
 __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const void* __restrict__ x, int x_bf16,
                                                              int M, int k, int splits, float* partial,
                                                              int* counters, void* __restrict__ y,
-                                                             int y_bf16, int n_total, int pre_rows = 0) {
+                                                             int y_bf16, int n_total, int pre_rows = 0,
+                                                             int xl = 0) {
   typedef TileStream<K, CB, NT, false> Stream;
   constexpr int NB = Stream::NB;
+  // Issue priority: the prologue and the split-K chain are latency-bound and short, the decode loop is VALU-bound
+  // and long.  The SIMD's arbiter prefers older waves among equals, so a CU's youngest workgroup would otherwise get
+  // few issue slots for its prologue and chain while older workgroups decode (gate_up 35.3 -> 34.3 us).
+  __builtin_amdgcn_s_setprio(2);
 
   const int Mp = P == 1 ? M : kGemvRows * ((M + kGemvRows - 1) / kGemvRows);  // staged rows; rows M .. Mp-1 are 0
   extern __shared__ __align__(16) uint8_t lds[];
@@ -278,7 +288,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 
   Stream stream;
   stream.init(sh.trellis, (k >> 4) * tn * 32 * K, tn, (blk - sh.blk0) * kGemvWaves + w, kb0, nb,
-              lds + gemv_a_bytes(Mp, NT) + w * Stream::LDS_BYTES, l);
+              lds + gemv_a_bytes(Mp, NT) + w * Stream::LDS_BYTES, l, sh.layout == EXL3_LAYOUT_BLOCKS, k >> 7);
   // Trellis blocks issued before the prologue.  Every workgroup's activation loads queue behind the trellis loads
   // the CU's workgroups issued before them, so the prologue (and with it the first MFMA) waits less with fewer early
   // blocks; the rest of the three in flight follow the prologue's barrier (layer set at one row: 79.2 -> 78.2 us).
@@ -349,6 +359,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 #pragma unroll
   for (int b = kEarly; b < 3 && b < NB; b++) stream.issue(b);
 
+  __builtin_amdgcn_s_setprio(0);
   // A row m = l % 16; rows m >= M read row M-1 (finite values) and only feed C rows that are never stored
   float4_t acc[P];
   if constexpr (P > 1) {
@@ -361,9 +372,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   }
 
 
-  // this split's partial; C layout: lane l holds rows 4(l/16) + r, column l % 16.  Partials cross XCDs (each XCD
-  // has its own L2), so they are written and read with device-scope coherence (sc1: write-through, no stale L2
-  // hits) instead of a device-scope fence, which would write back this XCD's whole L2.
+  __builtin_amdgcn_s_setprio(2);
+  // this split's partial; C layout: lane l holds rows 4(l/16) + r, column l % 16.  Each XCD has its own L2.  With
+  // xl (the host's check that workgroups whose linear ids agree mod 8 run on one XCD, and a column-block count that
+  // is a multiple of 8: all splits of a column block then share an XCD) the partials, the arrival counter and the
+  // reduce stay in that XCD's L2: plain stores, L2 atomics, loads that bypass only the L1.  Otherwise they are
+  // written and read with device-scope coherence (sc1: write-through, no stale L2 hits) instead of a device-scope
+  // fence, which would write back this XCD's whole L2.
   const int col_blk = blk * 128;  // first column of the block in y / partial
   const __amdgpu_buffer_rsrc_t prsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)partial, (short)0, splits * M * n_total * 4, 0x00020000);
@@ -373,13 +388,18 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int m = kGemvRows * p + 4 * j + r;
-      if (m < M)
-        __hip_atomic_store(pdst + (size_t)m * n_total, acc[p][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (m < M) {
+        if (xl)
+          __hip_atomic_store(pdst + (size_t)m * n_total, acc[p][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else
+          __hip_atomic_store(pdst + (size_t)m * n_total, acc[p][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this thread's partial stores are at the coherence point
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&counters[blk], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = xl ? __hip_atomic_fetch_add(&counters[blk], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                        : __hip_atomic_fetch_add(&counters[blk], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev == splits - 1;
   }
   __syncthreads();
@@ -403,10 +423,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
         float4_t v[8];
 #pragma unroll
         for (int i = 0; i < 8; i++)
-          v[i] = p0 + i * G < splits ? __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                        prsrc, base + (p0 + i * G) * pstride, 0,
-                                                                        kCoherentDevice))
-                                     : float4_t{0.f, 0.f, 0.f, 0.f};
+          v[i] = p0 + i * G >= splits ? float4_t{0.f, 0.f, 0.f, 0.f}
+                 : xl ? __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                            prsrc, base + (p0 + i * G) * pstride, 0, kBypassL1))
+                      : __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                            prsrc, base + (p0 + i * G) * pstride, 0, kCoherentDevice));
 #pragma unroll
         for (int i = 0; i < 8; i++)
           if (p0 + i * G < splits) a += v[i];
@@ -429,7 +450,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
     }
     __syncthreads();  // the next pass reuses red
   }
-  if (tid == 0) __hip_atomic_store(&counters[blk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    if (xl)
+      __hip_atomic_store(&counters[blk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+      __hip_atomic_store(&counters[blk], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---- host side --------------------------------------------------------------------------------------------------
@@ -526,6 +552,9 @@ static int build_shards(const exl3_shard* shards, int nshards, int k, int K, Sha
     sa->suh[s] = static_cast<const uint16_t*>(sh.suh);
     sa->svh[s] = static_cast<const uint16_t*>(sh.svh);
     sa->tn[s] = sh.n / 16;
+    EXL3_CHECK_ARG(sh.layout == EXL3_LAYOUT_STORED || sh.layout == EXL3_LAYOUT_BLOCKS, "shard %d: layout %d", s,
+                   sh.layout);
+    sa->layout[s] = sh.layout;
     sa->col0[s] = col;
     sa->blk0[s] = blk;
     col += sh.n;
@@ -584,6 +613,64 @@ static size_t gemv_workspace_bytes(int rows, int k, int n_total, int K, int laun
          gemv_pre_bytes(rows, k, n_total);
 }
 
+// ---- split-K chain inside one XCD ---------------------------------------------------------------------------
+// The launches' grids are x = column block (fastest), y = k-split, so the splits of a column block have linear
+// workgroup ids that agree mod the column-block count.  When workgroups whose ids agree mod 8 run on one XCD (the
+// hardware hands workgroup i to XCD i mod 8 on an 8-XCD part; the same holds with 1, 2 or 4 XCDs per device) and the
+// column-block count is a multiple of 8, every split of a column block runs on one XCD and its chain can stay in
+// that XCD's L2.  exl3_init_device checks the first property with a probe launch; until it has passed on some
+// device of the process, every chain uses device-coherent accesses.
+static std::atomic<int> g_xcd_groups_ok{0};
+
+__global__ __launch_bounds__(64) void xcd_probe_kernel(int* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xF);  // HW_REG_XCC_ID
+}
+
+int xcd_probe(int device) {
+  constexpr int kProbeWgs = 4096;
+  int cur = 0;
+  EXL3_CHECK_HIP(hipGetDevice(&cur));
+  if (cur != device) EXL3_CHECK_HIP(hipSetDevice(device));
+  int cus = 0;
+  EXL3_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  const int xcds = std::max(1, std::min(8, cus / 32));  // 32 CUs per XCD on gfx950
+  int* d = nullptr;
+  hipError_t e = hipMalloc(&d, kProbeWgs * sizeof(int));
+  int ok = 0;
+  if (e == hipSuccess) {
+    xcd_probe_kernel<<<kProbeWgs, 64>>>(d);
+    e = hipGetLastError();
+    std::vector<int> h(kProbeWgs);
+    if (e == hipSuccess) e = hipMemcpy(h.data(), d, kProbeWgs * sizeof(int), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) {
+      // the ids that agree mod 8 share an XCD, and the first 8 cover as many XCDs as the device has (a register that
+      // read the same value everywhere would otherwise pass)
+      ok = 1;
+      for (int i = 8; i < kProbeWgs; i++) ok &= h[i] == h[i % 8];
+      int distinct = 0;
+      for (int i = 0; i < 8; i++) {
+        bool seen = false;
+        for (int q = 0; q < i; q++) seen |= h[q] == h[i];
+        distinct += !seen;
+      }
+      ok &= distinct == xcds;
+    }
+    hipFree(d);
+  }
+  if (cur != device) (void)hipSetDevice(cur);
+  if (e != hipSuccess) return set_error(EXL3_ERR_HIP, "exl3_init_device: XCD probe: %s", hipGetErrorString(e));
+  if (ok) g_xcd_groups_ok.store(1);
+  return EXL3_OK;
+}
+
+static int xcd_local_chain(int nblk) {
+  static const bool off = [] {
+    const char* e = getenv("EXL3_GEMV_XCD_LOCAL");
+    return e && atoi(e) == 0;
+  }();
+  return !off && nblk % 8 == 0 && g_xcd_groups_ok.load(std::memory_order_relaxed) ? 1 : 0;
+}
+
 // launch_rows: 64 (two or four row groups per decoded tile past 16 rows; rotated launches only) or 16.  The
 // workspace is checked here against the plans of exactly these launches (every entry point's size function sizes the
 // same plans): a short workspace returns EXL3_ERR_INVALID before anything is launched.
@@ -617,12 +704,13 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
                    "%s: a launch of %d rows needs %zu bytes of partials, the workspace plan holds %zu", what, M,
                    (size_t)pl.splits * M * n_total * sizeof(float), partial_room);
     const dim3 grid(n_total / 128, pl.splits);
+    const int xl = xcd_local_chain(n_total / 128);
     const void* xr = static_cast<const uint8_t*>(pre ? (const void*)xh : x) + (size_t)r0 * k * 2;
     void* yr = static_cast<uint8_t*>(y) + (size_t)r0 * n_total * 2;
     bool ok = false;
 #define EXL3_GEMV_PAIR(NTV, PREV)                                                                                    \
   ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, NTV, PREV, 2><<<grid, kGemvThreads, pl.lds, st>>>(      \
-      sa, xr, PREV ? 0 : (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows)));
+      sa, xr, PREV ? 0 : (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows, xl)));
     if (pair) {  /* two row groups: the plan's LDS for 32 staged rows allows NT <= 32 */
       if (pl.nt == 16 && pre)
         EXL3_GEMV_PAIR(16, true)
@@ -637,7 +725,7 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
     // four row groups (narrow layers only, gemv_launch_rows): 64 staged rows at NT = 16 fit the default LDS
 #define EXL3_GEMV_QUAD(PREV)                                                                                         \
   ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, 16, PREV, 4><<<grid, kGemvThreads, pl.lds, st>>>(       \
-      sa, xr, PREV ? 0 : (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows)));
+      sa, xr, PREV ? 0 : (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows, xl)));
     if (quad) {
       if (pl.nt != 16) return set_error(EXL3_ERR_INVALID, "four-group GEMV planned at NT = %d", pl.nt);
       if (pre)
@@ -651,13 +739,13 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
     if (pre) /* the plan gives at most 32 with prepared rows */                                                      \
       ok = EXL3_DISPATCH_K_CB(K, cb, (gemv_kernel<kK, kCB, true, (NTV > 32 ? 32 : NTV), true><<<grid, kGemvThreads,  \
                                                                                              pl.lds, st>>>(          \
-          sa, xr, 0, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows)));                          \
+          sa, xr, 0, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, rows, xl)));                          \
     else if (rotate)                                                                                                 \
       ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, NTV><<<grid, kGemvThreads, pl.lds, st>>>(           \
-          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, 0, xl));                \
     else                                                                                                             \
       ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false, NTV><<<grid, kGemvThreads, pl.lds, st>>>(          \
-          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, 0, xl));                \
   }
     EXL3_GEMV_LAUNCH(16)
     EXL3_GEMV_LAUNCH(32)
@@ -668,10 +756,10 @@ static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_b
   if (!pair && !quad && !pre && pl.nt == NTV) {                                                                      \
     if (rotate)                                                                                                      \
       ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, true, NTV><<<grid, kGemvThreads, pl.lds, st>>>(           \
-          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, 0, xl));                \
     else                                                                                                             \
       ok = EXL3_DISPATCH_K_CB(K, cb, gemv_kernel<kK, kCB, false, NTV><<<grid, kGemvThreads, pl.lds, st>>>(          \
-          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total));                       \
+          sa, xr, (int)x_bf16, M, k, pl.splits, partial, counters, yr, (int)y_bf16, n_total, 0, xl));                \
   }
     EXL3_GEMV_FEW(24)
     EXL3_GEMV_FEW(40)
@@ -743,26 +831,60 @@ extern "C" int exl3_reconstruct(const void* trellis, int k, int n, int K, int co
   return EXL3_OK;
 }
 
-// The load-time layout of the kernels is the stored one (each lane reads its two trellis words straight from the tile
-// as stored; a tile-column-major layout measured no faster), so the repack and its inverse are the identity on the
-// bytes: a device copy, or nothing when the output is the input.
-static int trellis_identity(const char* what, const void* in, int k, int n, int K, void* out, void* stream) {
+// ---- load-time layout (EXL3_LAYOUT_BLOCKS) -----------------------------------------------------------------------
+// Tile (i, j) of the stored [k/16][n/16] tile grid goes to unit (j / 8, i / 8), position (j % 8) 8 + i % 8 of the unit:
+// each (128-column block, 128-row block) unit is one contiguous run of 64 tiles, units in column block major order,
+// and the 8 tiles of one tile column inside a unit are adjacent.  A workgroup of the balanced GEMV then reads one
+// contiguous run (its units of a column block follow each other), each wave 256K contiguous bytes per unit.
+// One thread moves one 16-byte piece; STORE_BLOCKS = false is the inverse map (unpack).
+__host__ __device__ inline size_t blocks_tile_index(int i, int j, int KB) {
+  return ((size_t)(j >> 3) * KB + (i >> 3)) * 64 + (j & 7) * 8 + (i & 7);
+}
+
+template <bool TO_BLOCKS>
+__global__ __launch_bounds__(256) void repack_blocks_kernel(const uint4* __restrict__ in, int tk, int tn, int K,
+                                                            uint4* __restrict__ out) {
+  const size_t piece = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece of the stored layout
+  const int per_tile = 2 * K;                                     // 16-byte pieces per tile
+  if (piece >= (size_t)tk * tn * per_tile) return;
+  const size_t tile = piece / per_tile;
+  const int part = (int)(piece - tile * per_tile);
+  const int i = (int)(tile / tn), j = (int)(tile - (size_t)i * tn);
+  const size_t b = blocks_tile_index(i, j, tk / 8) * per_tile + part;
+  if (TO_BLOCKS)
+    out[b] = in[piece];
+  else
+    out[piece] = in[b];
+}
+
+static int trellis_relayout(const char* what, bool to_blocks, const void* in, int k, int n, int K, void* out,
+                            void* stream) {
   EXL3_CHECK_ARG(in && out, "%s: null pointer", what);
+  EXL3_CHECK_ARG(in != out, "%s: the output must not alias the input", what);
   EXL3_CHECK_ARG(valid_bits(K), "%s: K = %d", what, K);
-  EXL3_CHECK_ARG(k > 0 && n > 0 && k % 16 == 0 && n % 16 == 0, "%s: k = %d, n = %d", what, k, n);
-  if (in == out) return EXL3_OK;
-  const size_t bytes = (size_t)k * n * K / 8;
-  const hipError_t e = hipMemcpyAsync(out, in, bytes, hipMemcpyDeviceToDevice, as_stream(stream));
-  if (e != hipSuccess) return set_error(EXL3_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  EXL3_CHECK_ARG(k > 0 && n > 0 && k % 128 == 0 && n % 128 == 0, "%s: k = %d, n = %d (multiples of 128)", what, k,
+                 n);
+  EXL3_CHECK_ARG((int64_t)k * n * K / 8 <= INT32_MAX, "%s: trellis exceeds the 2 GiB range", what);
+  EXL3_CHECK_ARG(((uintptr_t)in | (uintptr_t)out) % 16 == 0, "%s: buffers must be 16-byte aligned", what);
+  const int tk = k / 16, tn = n / 16;
+  const size_t pieces = (size_t)tk * tn * 2 * K;
+  const dim3 grid((unsigned)((pieces + 255) / 256));
+  if (to_blocks)
+    repack_blocks_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(static_cast<const uint4*>(in), tk, tn, K,
+                                                                     static_cast<uint4*>(out));
+  else
+    repack_blocks_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(static_cast<const uint4*>(in), tk, tn, K,
+                                                                      static_cast<uint4*>(out));
+  EXL3_CHECK_LAUNCH();
   return EXL3_OK;
 }
 
 extern "C" int exl3_repack_trellis(const void* trellis, int k, int n, int K, void* out, void* stream) {
-  return trellis_identity("exl3_repack_trellis", trellis, k, n, K, out, stream);
+  return trellis_relayout("exl3_repack_trellis", true, trellis, k, n, K, out, stream);
 }
 
 extern "C" int exl3_unpack_trellis(const void* packed, int k, int n, int K, void* out, void* stream) {
-  return trellis_identity("exl3_unpack_trellis", packed, k, n, K, out, stream);
+  return trellis_relayout("exl3_unpack_trellis", false, packed, k, n, K, out, stream);
 }
 
 extern "C" int exl3_had_in_group(const void* x, int x_bf16, int rows, int k, const void* suh_cat, int shards,

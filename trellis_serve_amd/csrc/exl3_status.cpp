@@ -32,5 +32,5 @@ extern "C" int exl3_init_device(int device) {
   if (std::string(prop.gcnArchName).rfind("gfx950", 0) != 0)
     return exl3::set_error(EXL3_ERR_UNSUPPORTED, "exl3_init_device: device %d is %s, this library is built for gfx950",
                            device, prop.gcnArchName);
-  return EXL3_OK;
+  return exl3::xcd_probe(device);
 }

@@ -45,21 +45,25 @@ struct TileStream {
   static constexpr int kOutOfRange = 0x7FFFFFF0;
 
   __amdgpu_buffer_rsrc_t rsrc;
-  int soff0, row_bytes, nb, lane;
+  int soff0, row_bytes, bstride, nb, lane;
   int goff[LPB];
   bool glive[LPB];
   u32x4_t buf[NB][LPB];
   uint8_t* stage;
   LaneGeo g;
 
-  // trellis: base of the matrix (int16 [k/16, n/16, 16K]); total_bytes: its size; tile_col: the wave's tile column;
-  // kb0: first 128-row block; nblocks: blocks holding data (1..NB); stage_lds: the wave's LDS_BYTES
+  // trellis: base of the matrix (int16 [k/16, n/16, 16K], or the EXL3_LAYOUT_BLOCKS form when `blocks`, with KB
+  // 128-row blocks); total_bytes: its size; tile_col: the wave's tile column; kb0: first 128-row block; nblocks:
+  // blocks holding data (1..NB); stage_lds: the wave's LDS_BYTES.  Both layouts put the block's 8 tiles of the
+  // column in the same stage order (tile row r at stage byte 32K r).
   __device__ __forceinline__ void init(const void* trellis, int total_bytes, int tn, int tile_col, int kb0,
-                                       int nblocks, uint8_t* stage_lds, int l) {
+                                       int nblocks, uint8_t* stage_lds, int l, bool blocks = false, int KB = 0) {
     const int tile_bytes = 32 * K;
     row_bytes = tn * tile_bytes;
     rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)trellis, (short)0, total_bytes, 0x00020000);
-    soff0 = kb0 * 8 * row_bytes + tile_col * tile_bytes;
+    soff0 = blocks ? ((tile_col >> 3) * KB + kb0) * 64 * tile_bytes + (tile_col & 7) * 8 * tile_bytes
+                   : kb0 * 8 * row_bytes + tile_col * tile_bytes;
+    bstride = blocks ? 64 * tile_bytes : 8 * row_bytes;
     nb = nblocks;
     lane = l;
     stage = stage_lds;
@@ -70,12 +74,12 @@ struct TileStream {
     for (int i = 0; i < LPB; i++) {
       const int L = i * 64 + l;
       glive[i] = L < CHUNKS;
-      goff[i] = glive[i] ? (L / (2 * K)) * row_bytes + (L % (2 * K)) * 16 : kOutOfRange;
+      goff[i] = !glive[i] ? kOutOfRange : blocks ? 16 * L : (L / (2 * K)) * row_bytes + (L % (2 * K)) * 16;
     }
   }
 
   __device__ __forceinline__ void issue(int b) {
-    const int so = soff0 + min(b, nb - 1) * 8 * row_bytes;
+    const int so = soff0 + min(b, nb - 1) * bstride;
 #pragma unroll
     for (int i = 0; i < LPB; i++)
       buf[b][i] = ALL_LANES || glive[i]

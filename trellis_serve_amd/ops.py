@@ -101,8 +101,18 @@ def _dev_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
+_initialised: set[int] = set()
+
+
 def _ws(kind: str, device: torch.device) -> _Workspace:
-    key = (kind, _dev_index(device))
+    idx = _dev_index(device)
+    if idx not in _initialised and not torch.cuda.is_current_stream_capturing():
+        # the device check, and the probe of the workgroup -> XCD assignment that lets split-K chains stay in one
+        # XCD's L2 (the reference's init_device, cuda/csrc/exl3_marlin.cu:537); a workspace is first taken (or
+        # reserved) before any capture
+        init_device(idx)
+        _initialised.add(idx)
+    key = (kind, idx)
     ws = _workspaces.get(key)
     if ws is None:
         ws = _workspaces[key] = _Workspace(kind, _KINDS[kind])
@@ -212,22 +222,26 @@ def reconstruct(trellis: torch.Tensor, codebook: int, out: torch.Tensor | None =
 
 
 def repack_trellis(trellis: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """The trellis in the layout the kernels read (the reference's repack_trellis, cuda/csrc/exl3_marlin.cu:344-381):
-    the stored int16 [k/16, n/16, 16K] layout itself, so the result is a copy (or `out` = the input: nothing to do)."""
-    return _trellis_identity(trellis, out, "exl3_repack_trellis")
+    """The trellis in the load-time layout (LAYOUT_BLOCKS; the reference's repack_trellis,
+    cuda/csrc/exl3_marlin.cu:344-381): the same bytes per tile, each (128-column block, 128-row block) unit of 64
+    tiles one contiguous run.  Same shape and dtype as the stored tensor; `out` must not be the input."""
+    return _trellis_relayout(trellis, out, "exl3_repack_trellis")
 
 
 def unpack_trellis(packed: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Inverse of repack_trellis (the reference's unpack_trellis, exl3_marlin.cu:384-408)."""
-    return _trellis_identity(packed, out, "exl3_unpack_trellis")
+    """Inverse of repack_trellis: the stored layout back, bit for bit (the reference's unpack_trellis,
+    exl3_marlin.cu:384-408)."""
+    return _trellis_relayout(packed, out, "exl3_unpack_trellis")
 
 
-def _trellis_identity(t: torch.Tensor, out: torch.Tensor | None, entry: str) -> torch.Tensor:
+def _trellis_relayout(t: torch.Tensor, out: torch.Tensor | None, entry: str) -> torch.Tensor:
     k, n, K = _check_trellis(t)
     if out is None:
         out = torch.empty_like(t)
     if out.shape != t.shape or out.dtype != torch.int16 or not out.is_contiguous() or out.device != t.device:
         raise ValueError(f"out must be a contiguous int16 {tuple(t.shape)} tensor on {t.device}")
+    if out.data_ptr() == t.data_ptr():
+        raise ValueError(f"{entry}: out must not be the input")
     _lib.check(getattr(_lib.load(), entry)(t.data_ptr(), k, n, K, out.data_ptr(), _stream(t.device)), entry)
     return out
 
@@ -283,7 +297,8 @@ def gemm_rotated(xh: torch.Tensor, trellis: torch.Tensor, codebook: int,
     return out
 
 
-def _shards(trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor], device: torch.device):
+def _shards(trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor], device: torch.device,
+            layout: int = _lib.LAYOUT_STORED):
     if not (1 <= len(trellis) <= _lib.MAX_SHARDS) or not (len(trellis) == len(suh) == len(svh)):
         raise ValueError(f"1..{_lib.MAX_SHARDS} shards with one trellis, suh and svh each")
     arr = (_lib.Exl3Shard * len(trellis))()
@@ -298,17 +313,17 @@ def _shards(trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torc
             raise ValueError(f"shard {i}: suh/svh sizes {su.numel()}/{sv.numel()} != {k}/{n}")
         if not (t.device == su.device == sv.device == device):
             raise ValueError(f"shard {i}: tensors on {t.device}/{su.device}/{sv.device}, x on {device}")
-        arr[i] = _lib.Exl3Shard(t.data_ptr(), su.data_ptr(), sv.data_ptr(), n)
+        arr[i] = _lib.Exl3Shard(t.data_ptr(), su.data_ptr(), sv.data_ptr(), n, int(layout))
     return arr, k0, K0
 
 
 def linear(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor],
-           codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+           codebook: int, out: torch.Tensor | None = None, layout: int = _lib.LAYOUT_STORED) -> torch.Tensor:
     """Fused group: y[..., sum n_s] = concat_s(Had(Had(x * suh_s) @ W_s) * svh_s), x fp16|bf16 [..., k], y in x's
     dtype (exl3_linear_marlin_multi_out, cuda/csrc/exl3_marlin.cu:507-527)."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"x must be fp16 or bf16, got {x.dtype}")
-    arr, k, K = _shards(trellis, suh, svh, x.device)
+    arr, k, K = _shards(trellis, suh, svh, x.device, layout)
     rows2d = x.reshape(-1, x.shape[-1]).contiguous()
     if rows2d.shape[1] != k:
         raise ValueError(f"x has {rows2d.shape[1]} features, the group expects {k}")
@@ -326,13 +341,13 @@ def linear(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor]
 
 
 def linear_prefill(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor], svh: list[torch.Tensor],
-                   codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+                   codebook: int, out: torch.Tensor | None = None, layout: int = _lib.LAYOUT_STORED) -> torch.Tensor:
     """Many-row form of `linear`: input rotations into a per-device workspace, then the fused decode-GEMM (weights
     decoded into LDS, fp16 MFMA).  Same result contract as `linear` (the reference's prefill branch,
     cuda/src/sglang_exl3/runtime/ops.py:87-95)."""
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError(f"x must be fp16 or bf16, got {x.dtype}")
-    arr, k, K = _shards(trellis, suh, svh, x.device)
+    arr, k, K = _shards(trellis, suh, svh, x.device, layout)
     rows2d = x.reshape(-1, x.shape[-1]).contiguous()
     if rows2d.shape[1] != k:
         raise ValueError(f"x has {rows2d.shape[1]} features, the group expects {k}")
