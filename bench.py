@@ -89,7 +89,7 @@ GRAPH_STEPS = 20
 SPINUP_S = 0.3   # untimed GPU work before the first timed replay (clock ramp after the idle layer-set build)
 
 
-def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int):
+def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int, layout: int = 0):
     """One graph holds S steps, rounds of the R copies (step i: the 4 fused linears on copy i mod R), S = R x up to
     GRAPH_STEPS // R rounds, no more than the steps asked for allow.  Replays it ceil(steps / S) times after
     ceil(warmup / S) untimed replays; returns (steps timed, ms per step, per-layer us per launch).  Per-layer times
@@ -104,7 +104,7 @@ def time_layer_set(torch, ops, sets, xs, steps: int, warmup: int):
         for r in copies:
             for nm in layer_names:
                 trs, suhs, svhs = sets[r][nm]
-                ops.linear(xs[nm], trs, suhs, svhs, CODEBOOK, out=outs[nm])
+                ops.linear(xs[nm], trs, suhs, svhs, CODEBOOK, out=outs[nm], layout=layout)
 
     def timed(g, reps, warm):
         for _ in range(warm):
@@ -707,6 +707,15 @@ def main() -> int:
     # warm secondary: one copy of the layer set (128 MB, inside the 256 MB MALL) replayed back to back
     _, warm_ms, _ = time_layer_set(torch, ops, sets[:1], xs_for(args.rows), max(20, args.steps // 4), args.warmup)
     print(f"[bench] M={args.rows} warm (one copy): {warm_ms * 1e3:.1f} us/step", file=sys.stderr, flush=True)
+    # the same step on the load-time BLOCKS layout (exl3_repack_trellis), same process and copies, timed like the
+    # headline; the stored-layout figures it is compared with are the headline's own
+    blocks_sets = [{nm: ([ops.repack_trellis(t) for t in trs], suhs, svhs) for nm, (trs, suhs, svhs) in st.items()}
+                   for st in sets]
+    _, blk_ms, blk_layer = time_layer_set(torch, ops, blocks_sets, xs_for(args.rows), main_r["steps"], args.warmup,
+                                          layout=1)
+    del blocks_sets
+    print(f"[bench] M={args.rows} BLOCKS layout: {blk_ms * 1e3:.1f} us/step per layer us "
+          f"{({k: round(v * 1e3, 1) for k, v in blk_layer.items()})}", file=sys.stderr, flush=True)
     # dominant kernel: the gate_up fused linear (one gemv_kernel launch); its per-launch time comes from HIP events
     # around graph replays of that layer alone
     kd, nd = LAYERS[DOMINANT]
@@ -745,6 +754,11 @@ def main() -> int:
                              "us_per_step": round(warm_ms * 1e3, 2)},
         "other_rows": {str(M): {"GB/s": round(r["gbs"], 1), "us_per_step": round(r["ms_per_step"] * 1e3, 2)}
                        for M, r in results.items() if M != args.rows},
+        "blocks_layout": {"GB/s": round(main_r["step_bytes"] / (blk_ms * 1e-3) / 1e9, 1),
+                          "us_per_step": round(blk_ms * 1e3, 2),
+                          "us_per_layer": {k: round(v * 1e3, 2) for k, v in blk_layer.items()},
+                          "what": "the headline step on the trellis repacked to EXL3_LAYOUT_BLOCKS at load, same "
+                                  "process; the stored-layout figures are value / us_per_layer"},
     }
     if not args.no_secondary:
         del sets
