@@ -63,7 +63,11 @@ typedef struct exl3_shard {
 /* ---- process / device ---------------------------------------------------------------------------------------- */
 int exl3_abi_version(void);
 const char* exl3_last_error(void);
-/* Checks that `device` is a gfx950.  Replaces init_device (cuda/csrc/exl3_marlin.cu:537). */
+/* Checks that `device` is a gfx950, then probes (one small launch, synchronous) that workgroups whose ids agree mod 8
+ * run on one XCD; once a probe has passed, decode-GEMV launches whose column-block count is a multiple of 8 keep their
+ * split-K partials and counters in that XCD's L2 (otherwise, and before any call here, they use device-coherent
+ * accesses; results are the same bits either way).  Call it before capturing graphs.  Replaces init_device
+ * (cuda/csrc/exl3_marlin.cu:537). */
 int exl3_init_device(int device);
 
 /* ---- decode (subsystem 1) ------------------------------------------------------------------------------------- */
@@ -71,10 +75,12 @@ int exl3_init_device(int device);
  * trellis_core.reference.reconstruct_inner (core/src/trellis_core/reference.py:102-115).  Replaces ExLlamaV3's
  * `reconstruct` as called at cuda/src/sglang_exl3/kernels/reference.py:71-76 and xpu/csrc/exl3_ops.sycl:536. */
 int exl3_reconstruct(const void* trellis, int k, int n, int K, int codebook, void* w_out, void* stream);
-/* Load-time repack of a stored trellis int16 [k/16][n/16][16K] into the layout the kernels read.  Replaces
- * repack_trellis (cuda/csrc/exl3_marlin.cu:344-381, called by prepare, cuda/src/sglang_exl3/kernels/marlin.py:65-76).
- * The gfx950 kernels read the stored layout itself, so the repacked form is the stored form: `out` receives a copy of
- * the k*n*K/8 bytes (nothing happens when out == trellis).  Lossless; exl3_unpack_trellis inverts it. */
+/* Load-time repack of a stored trellis int16 [k/16][n/16][16K] (k, n multiples of 128) into EXL3_LAYOUT_BLOCKS
+ * (k*n*K/8 bytes, a permutation of whole tiles; out must not alias the input; both 16-byte aligned).  Lossless;
+ * exl3_unpack_trellis inverts it bit for bit.  exl3_linear, exl3_linear_noalloc and exl3_linear_prefill read a
+ * repacked shard when its `layout` says so (same results); exl3_reconstruct, exl3_gemm_rotated and the MoE entry
+ * points read the stored layout.  Replaces repack_trellis (cuda/csrc/exl3_marlin.cu:344-381, called by prepare,
+ * cuda/src/sglang_exl3/kernels/marlin.py:65-76). */
 int exl3_repack_trellis(const void* trellis, int k, int n, int K, void* out, void* stream);
 /* Inverse of exl3_repack_trellis: the stored layout back.  Replaces unpack_trellis (exl3_marlin.cu:384-408). */
 int exl3_unpack_trellis(const void* packed, int k, int n, int K, void* out, void* stream);
