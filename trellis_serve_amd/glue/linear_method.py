@@ -8,7 +8,8 @@ xpu/exl3xpu/vllm_plugin.py:150-261):
   process_weights_after_loading
                    one checked Exl3Matrix per source matrix (ordered by output partition), installed in resident form.
   apply            x fp16|bf16 [..., k] -> [..., sum of output widths] in x's dtype.
-The trellis stays in its stored layout (the kernels read it directly): nothing is repacked or pre-decoded.
+The trellis stays in its stored layout (the kernels read it directly; the BLOCKS layout of `ops.repack_trellis`
+measures the same, so nothing is copied at load) and nothing is pre-decoded.
 
 What a source matrix must look like comes from the checkpoint headers (`infos`, one MatrixInfo per source in output
 order) or, for a vLLM model whose directory is not local, from the declared bitrate only (`declared_bits`): the

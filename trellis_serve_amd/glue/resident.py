@@ -3,8 +3,8 @@ their `apply` runs, the same for SGLang and vLLM.
 
 Dense (fused) linears keep one trellis, suh and svh buffer per source matrix, registered on the layer as
 `exl3_{trellis,suh,svh}_{i}` (the buffers the reference registers, cuda/src/sglang_exl3/sglang_glue/linear.py:
-145-152).  They are the only copy: the kernels read the stored layout, so nothing is repacked and pointers are taken
-per call.  Consecutive source matrices with one bitrate and codebook run as one launch (up to EXL3_MAX_SHARDS), the
+145-152).  They are the only copy: the kernels read the stored layout (the load-time BLOCKS layout of
+`ops.repack_trellis` measures the same, so no copy is made at load) and pointers are taken per call.  Consecutive source matrices with one bitrate and codebook run as one launch (up to EXL3_MAX_SHARDS), the
 fused-group launch of cuda/csrc/exl3_marlin.cu:507-527.
 
 Routed experts keep the stacked [E, ...] tensors `exl3_moe_forward` reads.
