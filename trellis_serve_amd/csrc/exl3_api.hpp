@@ -45,6 +45,8 @@ int prefill_plain_gemm(const void* xh, int rows, int k, const void* trellis, int
 // exl3_init_device's probe of the workgroup -> XCD assignment (exl3_linear.hip): enables split-K chains that stay
 // in one XCD's L2
 int xcd_probe(int device);
+// whether a probe has passed (and EXL3_GEMV_XCD_LOCAL is not 0): workgroups whose ids agree mod 8 share an XCD
+bool xcd_groups_ok();
 
 inline bool valid_bits(int K) { return K == 2 || K == 3 || K == 4 || K == 5 || K == 6 || K == 8; }
 inline bool valid_cb(int cb) { return cb >= 0 && cb <= 2; }

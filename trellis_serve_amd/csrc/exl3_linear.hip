@@ -663,13 +663,15 @@ int xcd_probe(int device) {
   return EXL3_OK;
 }
 
-static int xcd_local_chain(int nblk) {
+bool xcd_groups_ok() {
   static const bool off = [] {
     const char* e = getenv("EXL3_GEMV_XCD_LOCAL");
     return e && atoi(e) == 0;
   }();
-  return !off && nblk % 8 == 0 && g_xcd_groups_ok.load(std::memory_order_relaxed) ? 1 : 0;
+  return !off && g_xcd_groups_ok.load(std::memory_order_relaxed) != 0;
 }
+
+static int xcd_local_chain(int nblk) { return nblk % 8 == 0 && xcd_groups_ok() ? 1 : 0; }
 
 // launch_rows: 64 (two or four row groups per decoded tile past 16 rows; rotated launches only) or 16.  The
 // workspace is checked here against the plans of exactly these launches (every entry point's size function sizes the

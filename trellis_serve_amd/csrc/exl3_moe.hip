@@ -225,8 +225,10 @@ __global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const vo
 template <int K, int CB, int PHASE, int P, bool PRE, int NT>
 __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) void moe_gemv_kernel(
     MoeArgs a, const void* __restrict__ x, int x_bf16, uint16_t* __restrict__ gu, uint16_t* __restrict__ pre_dn_out,
-    uint16_t* __restrict__ dn, float* partial, int* counters, int splits, int chunks) {
+    uint16_t* __restrict__ dn, float* partial, int* counters, int splits, int chunks, int xl) {
   typedef TileStream<K, CB, NT, PRE> Stream;  // the prepared-row chunk pipeline needs every lane loading
+  // issue priority as in the dense GEMV: the short latency-bound prologue and split-K chain above the decode loop
+  __builtin_amdgcn_s_setprio(2);
   constexpr int NB = Stream::NB;
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int last_flag;
@@ -284,6 +286,7 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
   uint8_t* stage = lds + kActBufs * kMoeRows * P * mstride * 2 + w * Stream::LDS_BYTES;
 
   // passes of up to 16 P slots; each decoded tile feeds the pass's `groups` 16-row MFMAs
+  __builtin_amdgcn_s_setprio(0);
   for (int c0 = 0; c0 < n_e; c0 += kMoeRows * P) {
     const int M = min(kMoeRows * P, n_e - c0);
     const int groups = (M + kMoeRows - 1) / kMoeRows;
@@ -393,18 +396,26 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
         __syncthreads();  // the next chunk or pass restages LDS
       }
     }
-    // this split's partial rows, device-coherent (read by the last split, possibly on another XCD)
+    // this split's partial rows: device-coherent (read by the last split, possibly on another XCD), or, with xl
+    // (the host found every split of this counter on one XCD: workgroup ids that agree mod 8, and a probe that saw
+    // such ids on one XCD), plain stores into that XCD's L2
     float* pdst = partial + (size_t)sp * a.slots * n_out + cb * 128 + w * 16 + c;
 #pragma unroll
     for (int p = 0; p < P; p++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = kMoeRows * p + 4 * j + r;
-        if (m < M)
-          __hip_atomic_store(pdst + (size_t)slot_at(c0 + m) * n_out, acc[p][r], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+        if (m < M) {
+          if (xl)
+            __hip_atomic_store(pdst + (size_t)slot_at(c0 + m) * n_out, acc[p][r], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+          else
+            __hip_atomic_store(pdst + (size_t)slot_at(c0 + m) * n_out, acc[p][r], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
   }
+  __builtin_amdgcn_s_setprio(2);
   // arrivals: the k-splits of this column block; gate/up with several tokens (GLU) -- the k-splits of the gate block
   // and of the up block of the same 128 columns, on one counter
   constexpr bool GLU = PHASE == 0 && PRE;
@@ -413,7 +424,8 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&counters[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = xl ? __hip_atomic_fetch_add(&counters[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                        : __hip_atomic_fetch_add(&counters[ctr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_flag = prev == arrivals - 1;
   }
   __syncthreads();
@@ -432,8 +444,12 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
         const int pp = p0 + i < splits ? p0 + i : 0;
         const uint64_t* src =
             reinterpret_cast<const uint64_t*>(partial + ((size_t)pp * a.slots + slot) * n_out + pcol);
-        const uint64_t lo = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t hi = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // (xl: this CU never read these lines before in this launch, and the L1 starts each launch empty, so the
+        // L2's copy is what a plain load returns)
+        const uint64_t lo = xl ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                               : __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t hi = xl ? __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                               : __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         v[i] = float4_t{__builtin_bit_cast(float, (uint32_t)lo), __builtin_bit_cast(float, (uint32_t)(lo >> 32)),
                         __builtin_bit_cast(float, (uint32_t)hi), __builtin_bit_cast(float, (uint32_t)(hi >> 32))};
       }
@@ -485,7 +501,12 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
       *reinterpret_cast<half4_t*>(out + (size_t)slot * n_out + col) = half4_t{o[0], o[1], o[2], o[3]};
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(&counters[ctr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    if (xl)
+      __hip_atomic_store(&counters[ctr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+      __hip_atomic_store(&counters[ctr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 template <bool Y_BF16>
@@ -609,9 +630,13 @@ static void launch_moe_gemv(const MoePlan& p, const MoePhase& ph, dim3 grid, con
                             int x_bf16, uint16_t* gu, uint16_t* pre_dn, uint16_t* dn, float* partial, int* counters,
                             hipStream_t st) {
   const dim3 g3(grid.x, grid.y, ph.splits);
+  // a counter's splits have workgroup ids grid.x * grid.y apart; gate/up with prepared rows (the GLU launch) also
+  // counts the up block I / 128 column blocks after the gate block on the same counter
+  const bool glu = PHASE == 0 && !p.slot_mode;
+  const int xl = xcd_groups_ok() && (grid.x * grid.y) % 8 == 0 && !(glu && (a.I / 128) % 8 != 0) ? 1 : 0;
 #define EXL3_MOE_GEMV(P_, PRE_)                                                                              \
   moe_gemv_kernel<K, CB, PHASE, P_, PRE_, 16><<<g3, kMoeThreads, moe_lds_bytes<K, P_, 16, PRE_>(), st>>>(    \
-      a, x, x_bf16, gu, pre_dn, dn, partial, counters, ph.splits, ph.chunks)
+      a, x, x_bf16, gu, pre_dn, dn, partial, counters, ph.splits, ph.chunks, xl)
   if (p.slot_mode)
     EXL3_MOE_GEMV(1, false);
   else if (p.groups == 4)
