@@ -635,6 +635,11 @@ def measure_traffic() -> dict | None:
             "fetch_scale": got["FETCH_SIZE"][2], "write_scale": got["WRITE_SIZE"][2]}
 
 
+def _lib_xcd_local() -> int:
+    from trellis_serve_amd import _lib
+    return _lib.load().exl3_xcd_local_chains()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -739,7 +744,8 @@ def main() -> int:
         "data": "synthetic (seeded uniform int16 trellis codes, +-1 fp16 signs, N(0,1) fp16 activations)",
         "config": {"workload": "27B-class dense layer set, K=3 bpw, MCG (BASELINE configs[1])",
                    "rows": args.rows, "layers": {k: [kk, ns] for k, (kk, ns) in LAYERS.items()},
-                   "copies": args.copies, "bytes_per_step": main_r["step_bytes"]},
+                   "copies": args.copies, "bytes_per_step": main_r["step_bytes"],
+                   "xcd_local_chains": bool(_lib_xcd_local())},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None if traffic is None else round(traffic["bytes"]),

@@ -69,6 +69,9 @@ const char* exl3_last_error(void);
  * accesses; results are the same bits either way).  Call it before capturing graphs.  Replaces init_device
  * (cuda/csrc/exl3_marlin.cu:537). */
 int exl3_init_device(int device);
+/* 1 when split-K chains may stay in one XCD's L2 (a probe of exl3_init_device passed and EXL3_GEMV_XCD_LOCAL is not
+ * 0), else 0.  No counterpart in the reference: it reports which chain the launches of this process use. */
+int exl3_xcd_local_chains(void);
 
 /* ---- decode (subsystem 1) ------------------------------------------------------------------------------------- */
 /* W_inner fp16 [k, n] = the decoded trellis (Hadamard domain, no sign vectors), bit-identical to

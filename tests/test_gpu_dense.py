@@ -369,6 +369,17 @@ def test_repacked_group_matches_oracle(coracle, K, cb):
             col += n
 
 
+def test_xcd_probe_enables_local_chains_on_a_whole_mi355x():
+    """exl3_init_device's probe: on a device with all 256 CUs (8 XCDs), workgroups whose ids agree mod 8 share an XCD,
+    so split-K chains of launches with a multiple of 8 column blocks stay in one XCD's L2."""
+    from trellis_serve_amd import _lib
+    _ops().init_device(0)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if cus != 256:
+        pytest.skip(f"{cus} CUs: not a whole MI355X")
+    assert _lib.load().exl3_xcd_local_chains() == 1
+
+
 def test_linear_is_deterministic():
     rng = np.random.default_rng(7)
     k, n, K, cb = 2048, 1024, 3, 1

@@ -54,6 +54,7 @@ _SIGNATURES: dict[str, tuple] = {
     "exl3_abi_version": (_I, []),
     "exl3_last_error": (ctypes.c_char_p, []),
     "exl3_init_device": (_I, [_I]),
+    "exl3_xcd_local_chains": (_I, []),
     "exl3_reconstruct": (_I, [_P, _I, _I, _I, _I, _P, _P]),
     "exl3_repack_trellis": (_I, [_P, _I, _I, _I, _P, _P]),
     "exl3_unpack_trellis": (_I, [_P, _I, _I, _I, _P, _P]),

@@ -820,6 +820,8 @@ static int scratch_of_stream_device(hipStream_t st, void** out) {
   return EXL3_OK;
 }
 
+extern "C" int exl3_xcd_local_chains(void) { return xcd_groups_ok() ? 1 : 0; }
+
 extern "C" int exl3_reconstruct(const void* trellis, int k, int n, int K, int codebook, void* w_out, void* stream) {
   EXL3_CHECK_ARG(trellis && w_out, "exl3_reconstruct: null pointer");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_reconstruct: K = %d / codebook = %d", K, codebook);
