@@ -27,11 +27,13 @@ __host__ __device__ constexpr int stream_lds_bytes(int K, bool all_lanes = false
   return all_lanes ? 2 * ((16 * K + 63) / 64) * 1024 : 2 * 256 * K;
 }
 
-// ALL_LANES: lanes past the last chunk still load -- from beyond the buffer's end, which reads zeros -- and write their
-// stage slot, so that no load or stage write is lane-conditional.  A lane-conditional load is a branch the compiler
-// must assume taken or skipped, which turns its in-order load waits into vmcnt(0) in a loop that keeps loads in
-// flight across iterations (the MoE chunk pipeline); straight-line callers (the dense GEMV) keep the lane mask, which
-// spends fewer address cycles (48 of 64 lanes at K = 3).
+// Every lane issues every gather: lanes past the last chunk read from beyond the buffer's end (zeros, no memory
+// request).  A lane-conditional load is a branch the compiler must assume taken or skipped, so the number of loads
+// younger than a given one becomes path-dependent and its in-order load waits turn into vmcnt(0): with the lane mask
+// (48 of 64 lanes at K = 3) the dense GEMV's first decode waited for all three blocks in flight and every later block
+// for the one issued after it (layer set at one row 80.1 -> 75.7 us, same call).
+// ALL_LANES: lanes past the last chunk also write their stage slot, so no stage write is lane-conditional either (the
+// MoE chunk pipeline, whose loop keeps loads in flight across iterations).
 template <int K, int CB, int NT, bool ALL_LANES = false>
 struct TileStream {
   static constexpr int NB = NT / 8;               // 128-row blocks
@@ -82,9 +84,7 @@ struct TileStream {
     const int so = soff0 + min(b, nb - 1) * bstride;
 #pragma unroll
     for (int i = 0; i < LPB; i++)
-      buf[b][i] = ALL_LANES || glive[i]
-                      ? __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, goff[i], so, 0))
-                      : u32x4_t{0, 0, 0, 0};
+      buf[b][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, goff[i], so, 0));
   }
 
   // the first three blocks; call before staging the activations so their latency overlaps
