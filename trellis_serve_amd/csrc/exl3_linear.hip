@@ -11,6 +11,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <mutex>
 #include <vector>
@@ -472,6 +473,9 @@ struct GemvPlan {
 // is written and read again and the last split's reduce reads all of them; one row group takes the equal-split rule
 // of gemv_plan and its own minimum
 constexpr int kGemvOneGroupWgs = 448;
+// one-group workgroups resident at once on MI355X: 256 CUs x 4 (8 waves of <= 64 VGPRs, < 40 KB of LDS each).  A
+// constant, so that the plan (and with it every workspace size) depends on the arguments alone.
+constexpr int kGemvOneGroupSlots = 256 * 4;
 static int gemv_target_wgs() {
   static const int env = [] {
     const char* e = getenv("EXL3_GEMV_TARGET_WGS");
@@ -493,13 +497,27 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K, bool pre = false) {
     // tile rows for >= 1536 workgroups below 8 rows, >= 768 from 8; same call): one row down 21.3 -> 18.6 us (32),
     // q/k/v 12.9 -> 11.9 (40), o 11.7 -> 11.0 (32), gate_up 33.7 -> 33.5 (40); 16 rows q/k/v 18.4 -> 16.7 (40),
     // o 16.2 -> 15.4 (32); 48-64 tile rows were no faster anywhere and slower on q/k/v and gate_up.
+    // When the longest such split gives more workgroups than run at once, the launch runs in rounds and the last one
+    // may leave most slots idle: then the candidate whose last round is fullest (workgroups / slots closest to a
+    // whole number from below) wins.  One row, same call, two rounds: gate_up 40 -> 32 tile rows (2.1 -> 2.7 rounds)
+    // 30.1-30.3 -> 29.8-30.1 us, down 32 -> 24 (1.3 -> 1.8 rounds) 18.0-18.1 -> 17.7-17.8 us; q/k/v and o (under one
+    // round) kept their splits, which measured best for them (40 / 32).
+    double best_fill = 0.0;
     for (int cand : {40, 32, 24}) {
       if (pre && cand != 32) continue;
       const int nbc = cand / 8, splits = (kb + nbc - 1) / nbc;
       if (splits * nbc * 50 <= kb * 51 && (size_t)nblk * splits >= kGemvOneGroupWgs &&
           gemv_lds_bytes(Ms, cand, K) <= kGemvMaxLds) {
-        nt = cand;
-        break;
+        const double rounds = (double)nblk * splits / kGemvOneGroupSlots;
+        if (best_fill == 0.0 && rounds <= 1.0) {  // the longest candidate fits one round: take it
+          nt = cand;
+          break;
+        }
+        const double fill = rounds <= 1.0 ? 1.0 : rounds / std::ceil(rounds);
+        if (fill > best_fill + 1e-9) {
+          best_fill = fill;
+          nt = cand;
+        }
       }
     }
     return {nt, (kb + nt / 8 - 1) / (nt / 8), (size_t)gemv_lds_bytes(Ms, nt, K)};
@@ -593,24 +611,27 @@ static int gemv_launch_rows(int k, int n_total, int launch_rows) {
 // workspace layout: [counter region][fp32 partials of the largest launch][rotated rows, when gemv_pre].
 // launch_rows: the entry point's rows per launch, 16 (exl3_gemm_rotated, exl3_linear_noalloc), or 64 where row groups
 // share each decoded tile (exl3_linear; gemv_launch_rows may lower it to 32).  A call's launches are the full ones
-// and the remainder, each with its own split plan: the partial region holds the larger of the two.
-static size_t gemv_launch_partial_bytes(int M, int rows, int k, int n_total, int K) {
-  return (size_t)gemv_plan(k, n_total, M, K, gemv_pre(rows, k, n_total)).splits * M * n_total * sizeof(float);
+// and the remainder, each with its own split plan: the partial region holds the larger of the two.  rotate: the
+// launches rotate their inputs (exl3_linear, exl3_linear_noalloc) and may then take prepared rows, whose split plan
+// differs; exl3_gemm_rotated's do not.
+static size_t gemv_launch_partial_bytes(int M, int rows, int k, int n_total, int K, bool rotate) {
+  const bool pre = rotate && gemv_pre(rows, k, n_total);
+  return (size_t)gemv_plan(k, n_total, M, K, pre).splits * M * n_total * sizeof(float);
 }
-static size_t gemv_partial_bytes(int rows, int k, int n_total, int K, int launch_rows) {
+static size_t gemv_partial_bytes(int rows, int k, int n_total, int K, int launch_rows, bool rotate) {
   size_t need = 0;
   launch_rows = gemv_launch_rows(k, n_total, launch_rows);
   for (int M : {std::min(rows, launch_rows), rows % launch_rows})
-    if (M > 0) need = std::max(need, gemv_launch_partial_bytes(M, rows, k, n_total, K));
+    if (M > 0) need = std::max(need, gemv_launch_partial_bytes(M, rows, k, n_total, K, rotate));
   return (need + 255) & ~(size_t)255;
 }
-static size_t gemv_pre_bytes(int rows, int k, int n_total) {
-  return gemv_pre(rows, k, n_total) ? (size_t)EXL3_MAX_SHARDS * rows * k * 2 : 0;
+static size_t gemv_pre_bytes(int rows, int k, int n_total, bool rotate) {
+  return rotate && gemv_pre(rows, k, n_total) ? (size_t)EXL3_MAX_SHARDS * rows * k * 2 : 0;
 }
 
-static size_t gemv_workspace_bytes(int rows, int k, int n_total, int K, int launch_rows) {
-  return counters_bytes(n_total) + gemv_partial_bytes(rows, k, n_total, K, launch_rows) +
-         gemv_pre_bytes(rows, k, n_total);
+static size_t gemv_workspace_bytes(int rows, int k, int n_total, int K, int launch_rows, bool rotate) {
+  return counters_bytes(n_total) + gemv_partial_bytes(rows, k, n_total, K, launch_rows, rotate) +
+         gemv_pre_bytes(rows, k, n_total, rotate);
 }
 
 // ---- split-K chain inside one XCD ---------------------------------------------------------------------------
@@ -679,15 +700,15 @@ static int xcd_local_chain(int nblk) { return nblk % 8 == 0 && xcd_groups_ok() ?
 static int launch_gemv(const ShardArgs& sa, const void* x, bool rotate, bool x_bf16, int rows, int k, int K, int cb,
                        int n_total, void* workspace, size_t workspace_bytes, void* y, bool y_bf16, hipStream_t st,
                        int launch_rows, const char* what) {
-  const size_t need = gemv_workspace_bytes(rows, k, n_total, K, launch_rows);
+  const size_t need = gemv_workspace_bytes(rows, k, n_total, K, launch_rows, rotate);
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "%s: workspace %zu bytes, need %zu", what, workspace_bytes,
                  need);
-  const size_t partial_room = gemv_partial_bytes(rows, k, n_total, K, launch_rows);
+  const size_t partial_room = gemv_partial_bytes(rows, k, n_total, K, launch_rows, rotate);
   int* counters = static_cast<int*>(workspace);
   float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total));
   const bool pre = rotate && gemv_pre(rows, k, n_total);
   uint16_t* xh = reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(workspace) + counters_bytes(n_total) +
-                                             gemv_partial_bytes(rows, k, n_total, K, launch_rows));
+                                             partial_room);
   if (pre) {
     const dim3 hgrid((unsigned)(((size_t)sa.count * rows * (k / 128) + 7) / 8));
     if (x_bf16)
@@ -933,7 +954,7 @@ extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int 
       !valid_bits(K))
     return 0;
   // exl3_linear's launches: up to 64 rows each (1, 2 or 4 row groups per decoded tile), then the remainder
-  return gemv_workspace_bytes(rows, k, n_total, K, kGemvQuadRows);
+  return gemv_workspace_bytes(rows, k, n_total, K, kGemvQuadRows, true);
 }
 
 extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards,
@@ -953,7 +974,7 @@ extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl
 extern "C" size_t exl3_gemm_rotated_workspace_bytes(int rows, int k, int n, int K) {
   if (rows <= 0 || k <= 0 || n <= 0 || k % 128 || n % 128 || n / 128 > kMaxCounters || !valid_bits(K)) return 0;
   if (rows >= kPrefillRows) return prefill_plain_workspace_bytes(rows, k, n);
-  return gemv_workspace_bytes(rows, k, n, K, kGemvRows);
+  return gemv_workspace_bytes(rows, k, n, K, kGemvRows, false);
 }
 
 // Rows are served by the kernel that serves the same row count in a linear: below kPrefillRows the decode-GEMV (one
@@ -991,7 +1012,7 @@ extern "C" int exl3_linear_noalloc(const void* x, int x_bf16, int rows, int k, c
   if (int rc = build_shards(shards_host, nshards, k, K, &sa, &n_total)) return rc;
   if (rows == 0) return EXL3_OK;
   // 16 rows per launch here (the scratch need of the two-row-group launches would be larger)
-  const size_t need = gemv_workspace_bytes(rows, k, n_total, K, kGemvRows);
+  const size_t need = gemv_workspace_bytes(rows, k, n_total, K, kGemvRows, true);
   EXL3_CHECK_ARG(need <= (size_t)EXL3_NOALLOC_SCRATCH_BYTES,
                  "exl3_linear_noalloc: %d rows of %d -> %d need %zu bytes of scratch, the library holds %zu; use "
                  "exl3_linear with a workspace", rows, k, n_total, need, (size_t)EXL3_NOALLOC_SCRATCH_BYTES);
