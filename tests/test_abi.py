@@ -136,6 +136,38 @@ def test_reported_workspace_sizes_cover_every_launch_plan(lib):
                         _lib.EXL3_ERR_INVALID, (K, k, n, rows)
 
 
+def test_one_group_split_plan_fills_its_last_round(lib):
+    """The decode-GEMV split plan at the configs[1] shapes, read back through the reported workspace size (counter
+    region + splits x rows x n x 4 bytes of partials, 256-byte aligned): the longest equal split of 40 / 32 / 24 tile
+    rows (5 / 4 / 3 blocks of 128 rows) with >= 448 workgroups, unless that needs more than one round of 1024
+    workgroups -- then the split whose last round is fullest.  A plan derived here independently of the library."""
+    counters = 256 * 1024
+    slots = 1024
+
+    def plan_splits(k, n):
+        kb, nblk = k // 128, n // 128
+        best = None
+        for nt in (40, 32, 24):
+            nbc = nt // 8
+            splits = -(-kb // nbc)
+            if splits * nbc * 50 > kb * 51 or nblk * splits < 448:
+                continue
+            rounds = nblk * splits / slots
+            if best is None and rounds <= 1:
+                return splits
+            fill = 1.0 if rounds <= 1 else rounds / -(-rounds // 1)
+            if best is None or fill > best[0] + 1e-9:
+                best = (fill, splits)
+        return best[1]
+
+    expect = {(5120, 8192): 8, (6144, 5120): 12, (5120, 34816): 10, (17408, 5120): 46}
+    for (k, n), splits in expect.items():
+        assert plan_splits(k, n) == splits, (k, n)
+        for rows in (1, 4, 7):
+            want = counters + ((splits * rows * n * 4 + 255) & ~255)
+            assert lib.exl3_linear_workspace_bytes(rows, k, n, 3) == want, (k, n, rows)
+
+
 def test_mixed_moe_entry_points_reject_bad_class_counts(lib):
     P, I = ctypes.c_void_p, ctypes.c_int
     maps, blocks = (P * 3)(1, 1, 1), (I * 3)(16, 16, 16)
