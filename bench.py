@@ -659,7 +659,7 @@ def main() -> int:
         return probe(args.probe, args.probe_launches)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} requested). "
-              "Sharding is described in DESIGN.md; run with --gpus 1.", file=sys.stderr)
+              "The value is one GPU's throughput; run with --gpus 1.", file=sys.stderr)
         return 2
 
     traffic = None
