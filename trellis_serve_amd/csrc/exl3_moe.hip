@@ -219,9 +219,10 @@ __global__ __launch_bounds__(256) void moe_route_prep_kernel(MoeArgs a, const vo
 
 // PRE: activations copied from prepared rows (gate/up with several tokens; down always); else the gate/up input
 // rotation is computed here (slot mode, one row).
-// The prepared-row kernels with P <= 2 and K <= 4 are held to 64 VGPRs (8 waves per SIMD), which they reach without
-// spilling; the others take what they need (P = 4 and K >= 5: 80-130 VGPRs; P = 4 is held to one workgroup per CU by
-// its LDS anyway).
+// The prepared-row kernels with P <= 2 and K <= 4 are held to 64 VGPRs (8 waves per SIMD): P = 1 fits without
+// spilling, P = 2 spills 6-8 VGPRs that live across the pass loop (stored before it, reloaded after its chunk loop,
+// none inside); the others take what they need (P = 4 and K >= 5: 80-130 VGPRs; P = 4 is held to one workgroup per CU
+// by its LDS anyway).
 template <int K, int CB, int PHASE, int P, bool PRE, int NT>
 __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) void moe_gemv_kernel(
     MoeArgs a, const void* __restrict__ x, int x_bf16, uint16_t* __restrict__ gu, uint16_t* __restrict__ pre_dn_out,
