@@ -9,6 +9,9 @@
  *   - each call returns EXL3_OK or an error code; exl3_last_error() then holds a message (thread-local).
  *     Where the reference raised (TORCH_CHECK -> RuntimeError), this library returns EXL3_ERR_INVALID and
  *     launches nothing.
+ *   - a call with zero rows (tokens, slots, sequences) launches nothing and returns EXL3_OK once its other
+ *     arguments check out; its activation, output and routing pointers may then be NULL (weights, sign vectors
+ *     and caches are still checked).
  *
  * The EXL3 format (core/src/trellis_core/format/spec.py:117-160): trellis int16 [k/16, n/16, 16K], K bits per
  * weight in {2,3,4,5,6,8}, k and n multiples of 128; suh fp16 [k], svh fp16 [n]; codebook 0 = 3INST, 1 = MCG,

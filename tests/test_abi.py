@@ -136,6 +136,38 @@ def test_reported_workspace_sizes_cover_every_launch_plan(lib):
                         _lib.EXL3_ERR_INVALID, (K, k, n, rows)
 
 
+def test_zero_rows_launch_nothing_and_accept_null_data_pointers(lib):
+    """Every entry point called with zero rows / tokens / slots / sequences returns EXL3_OK before any HIP call, with
+    its activation, output and routing pointers NULL (weights and caches still given): an empty batch is a no-op,
+    so these run without a GPU.  Bad shapes at zero size are still rejected."""
+    P, N = 0x1000, None
+    shard = (_lib.Exl3Shard * 1)(_lib.Exl3Shard(P, P, P, 256))
+    ok = _lib.EXL3_OK
+    assert lib.exl3_linear(N, 0, 0, 256, shard, 1, 3, 1, N, 0, N, 0, None) == ok, lib.exl3_last_error()
+    assert lib.exl3_linear_noalloc(N, 0, 0, 256, shard, 1, 3, 1, N, 0, None) == ok, lib.exl3_last_error()
+    assert lib.exl3_linear_prefill(N, 0, 0, 256, shard, 1, 3, 1, N, 0, N, 0, None) == ok, lib.exl3_last_error()
+    assert lib.exl3_gemm_rotated(N, 0, 256, P, 256, 3, 1, N, N, 0, None) == ok, lib.exl3_last_error()
+    assert lib.exl3_had_in_group(N, 0, 0, 256, P, 1, N, None) == ok, lib.exl3_last_error()
+    assert lib.exl3_had_out_into(N, 0, 256, P, N, 0, 256, 0, None) == ok, lib.exl3_last_error()
+    wts = _lib.Exl3MoeWeights(*([P] * 9))
+    assert lib.exl3_moe_forward(N, 0, 0, 256, N, N, 8, 16, 128, ctypes.byref(wts), 3, 3, 1, N, 0, N, 0, None) == ok, \
+        lib.exl3_last_error()
+    assert lib.exl3_moe_combine(N, N, N, 0, 8, 256, 16, N, 0, None) == ok, lib.exl3_last_error()
+    suh = (ctypes.c_void_p * 2)(P, P)
+    assert lib.exl3_moe_had_in(N, 0, 0, 256, N, 8, 16, suh, 2, N, None) == ok, lib.exl3_last_error()
+    tr = (ctypes.c_void_p * 1)(P)
+    assert lib.exl3_moe_gemm(N, 0, 256, tr, None, 1, 256, N, N, N, 4, 16, 16, 3, 1, N, N, 0, None) == ok, \
+        lib.exl3_last_error()
+    assert lib.exl3_moe_glu_had_in(N, 0, 256, N, 16, P, N, N, None) == ok, lib.exl3_last_error()
+    assert lib.exl3_kv_decode_attention(N, P, P, P, P, 4, N, 4, N, 0, 40, 8, 128, 16, 8, 0.1, N, N, 0, None) == ok, \
+        lib.exl3_last_error()
+    # zero size does not excuse bad shapes or missing weights
+    assert lib.exl3_linear(N, 0, 0, 200, shard, 1, 3, 1, N, 0, N, 0, None) == _lib.EXL3_ERR_INVALID
+    assert lib.exl3_gemm_rotated(N, 0, 256, N, 256, 3, 1, N, N, 0, None) == _lib.EXL3_ERR_INVALID
+    assert lib.exl3_kv_decode_attention(N, N, P, P, P, 4, N, 4, N, 0, 40, 8, 128, 16, 8, 0.1, N, N, 0, None) == \
+        _lib.EXL3_ERR_INVALID
+
+
 def test_one_group_split_plan_fills_its_last_round(lib):
     """The decode-GEMV split plan at the configs[1] shapes, read back through the reported workspace size (counter
     region + splits x rows x n x 4 bytes of partials, 256-byte aligned): the longest equal split of 40 / 32 / 24 tile

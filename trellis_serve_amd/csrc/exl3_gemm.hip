@@ -728,7 +728,7 @@ using namespace exl3;
 extern "C" int exl3_linear_prefill(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host,
                                    int nshards, int K, int codebook, void* y, int y_bf16, void* workspace,
                                    size_t workspace_bytes, void* stream) {
-  EXL3_CHECK_ARG(x && y && shards_host, "exl3_linear_prefill: null pointer");
+  EXL3_CHECK_ARG((rows == 0 || (x && y)) && shards_host, "exl3_linear_prefill: null pointer");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_linear_prefill: K = %d / codebook = %d", K, codebook);
   EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_linear_prefill: rows = %d, k = %d", rows, k);
   EXL3_CHECK_ARG(nshards >= 1 && nshards <= EXL3_MAX_SHARDS, "exl3_linear_prefill: nshards = %d", nshards);

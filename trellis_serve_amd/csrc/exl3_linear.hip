@@ -914,7 +914,7 @@ extern "C" int exl3_unpack_trellis(const void* packed, int k, int n, int K, void
 
 extern "C" int exl3_had_in_group(const void* x, int x_bf16, int rows, int k, const void* suh_cat, int shards,
                                  void* xh, void* stream) {
-  EXL3_CHECK_ARG(x && suh_cat && xh, "exl3_had_in_group: null pointer");
+  EXL3_CHECK_ARG((rows == 0 || (x && xh)) && suh_cat, "exl3_had_in_group: null pointer");
   EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_had_in_group: rows = %d, k = %d", rows, k);
   EXL3_CHECK_ARG(shards >= 1 && shards <= EXL3_MAX_SHARDS, "exl3_had_in_group: shards = %d", shards);
   if (rows == 0) return EXL3_OK;
@@ -932,7 +932,7 @@ extern "C" int exl3_had_in_group(const void* x, int x_bf16, int rows, int k, con
 
 extern "C" int exl3_had_out_into(const void* y, int rows, int n, const void* svh, void* out, int out_bf16, int ld_out,
                                  int col0, void* stream) {
-  EXL3_CHECK_ARG(y && svh && out, "exl3_had_out_into: null pointer");
+  EXL3_CHECK_ARG((rows == 0 || (y && out)) && svh, "exl3_had_out_into: null pointer");
   EXL3_CHECK_ARG(rows >= 0 && n > 0 && n % 128 == 0, "exl3_had_out_into: rows = %d, n = %d", rows, n);
   EXL3_CHECK_ARG(col0 >= 0 && col0 % 4 == 0 && ld_out >= col0 + n && ld_out % 4 == 0,
                  "exl3_had_out_into: col0 = %d, n = %d, ld_out = %d (4-aligned, in range)", col0, n, ld_out);
@@ -960,7 +960,7 @@ extern "C" size_t exl3_linear_workspace_bytes(int rows, int k, int n_total, int 
 extern "C" int exl3_linear(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host, int nshards,
                            int K, int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes,
                            void* stream) {
-  EXL3_CHECK_ARG(x && y, "exl3_linear: null x / y");
+  EXL3_CHECK_ARG(rows == 0 || (x && y), "exl3_linear: null x / y");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_linear: K = %d / codebook = %d", K, codebook);
   EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_linear: rows = %d, k = %d", rows, k);
   ShardArgs sa;
@@ -981,7 +981,7 @@ extern "C" size_t exl3_gemm_rotated_workspace_bytes(int rows, int k, int n, int 
 // 16-row group per launch, two decoded tiles per MFMA), from there the prefill decode-GEMM, both without rotations.
 extern "C" int exl3_gemm_rotated(const void* xh, int rows, int k, const void* trellis, int n, int K, int codebook,
                                  void* out, void* workspace, size_t workspace_bytes, void* stream) {
-  EXL3_CHECK_ARG(xh && trellis && out, "exl3_gemm_rotated: null pointer");
+  EXL3_CHECK_ARG((rows == 0 || (xh && out)) && trellis, "exl3_gemm_rotated: null pointer");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_gemm_rotated: K = %d / codebook = %d", K, codebook);
   EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0 && n > 0 && n % 128 == 0,
                  "exl3_gemm_rotated: rows = %d, k = %d, n = %d", rows, k, n);
@@ -1004,7 +1004,7 @@ extern "C" size_t exl3_linear_noalloc_max_bytes(void) { return EXL3_NOALLOC_SCRA
 
 extern "C" int exl3_linear_noalloc(const void* x, int x_bf16, int rows, int k, const exl3_shard* shards_host,
                                    int nshards, int K, int codebook, void* y, int y_bf16, void* stream) {
-  EXL3_CHECK_ARG(x && y, "exl3_linear_noalloc: null x / y");
+  EXL3_CHECK_ARG(rows == 0 || (x && y), "exl3_linear_noalloc: null x / y");
   EXL3_CHECK_ARG(valid_bits(K) && valid_cb(codebook), "exl3_linear_noalloc: K = %d / codebook = %d", K, codebook);
   EXL3_CHECK_ARG(rows >= 0 && k > 0 && k % 128 == 0, "exl3_linear_noalloc: rows = %d, k = %d", rows, k);
   ShardArgs sa;

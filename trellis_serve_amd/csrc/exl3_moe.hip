@@ -688,7 +688,7 @@ static int moe_forward_impl(const char* what, const void* x, int x_bf16, int tok
                             const void* topk_weights, int top_k, int num_experts, int inter, const MoeClass* cls,
                             int ncls, int codebook, void* y, int y_bf16, void* workspace, size_t workspace_bytes,
                             hipStream_t st) {
-  EXL3_CHECK_ARG(x && y && topk_ids && topk_weights, "%s: null pointer", what);
+  EXL3_CHECK_ARG(tokens == 0 || (x && y && topk_ids && topk_weights), "%s: null pointer", what);
   EXL3_CHECK_ARG(valid_cb(codebook), "%s: codebook = %d", what, codebook);
   EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && top_k <= kMoeMaxTopK, "%s: tokens = %d, top_k = %d", what, tokens,
                  top_k);
@@ -852,7 +852,7 @@ extern "C" int exl3_moe_forward_classes(const void* x, int x_bf16, int tokens, i
 
 extern "C" int exl3_moe_combine(const void* yd, const float* topk_weights, const int* topk_ids, int tokens, int top_k,
                                 int hidden, int num_experts, void* y, int y_bf16, void* stream) {
-  EXL3_CHECK_ARG(yd && topk_weights && topk_ids && y, "exl3_moe_combine: null pointer");
+  EXL3_CHECK_ARG(tokens == 0 || (yd && topk_weights && topk_ids && y), "exl3_moe_combine: null pointer");
   EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && hidden > 0 && hidden % 128 == 0 && num_experts >= 1,
                  "exl3_moe_combine: tokens = %d, top_k = %d, hidden = %d, num_experts = %d", tokens, top_k, hidden,
                  num_experts);

@@ -332,7 +332,7 @@ extern "C" int exl3_moe_align_classes(const int* topk_ids, int slots, int num_ex
                                       int* const* expert_ids_host, const int* max_blocks_host,
                                       int* const* num_post_padded_host, void* stream) {
   const char* what = nclasses == 1 ? "exl3_moe_align" : "exl3_moe_align_classes";
-  EXL3_CHECK_ARG(topk_ids, "%s: null pointer", what);
+  EXL3_CHECK_ARG(slots == 0 || topk_ids, "%s: null pointer", what);
   EXL3_CHECK_ARG(nclasses >= 1 && nclasses <= EXL3_MOE_MAX_CLASSES, "%s: nclasses = %d (1..%d)", what, nclasses,
                  EXL3_MOE_MAX_CLASSES);
   EXL3_CHECK_ARG(expert_maps_host && blocks_host && sorted_ids_host && caps_host && expert_ids_host &&
@@ -359,7 +359,7 @@ extern "C" int exl3_moe_align_classes(const int* topk_ids, int slots, int num_ex
 
 extern "C" int exl3_moe_had_in(const void* x, int x_bf16, int tokens, int k, const int* topk_ids, int top_k,
                                int num_experts, const void* const* suh, int shards, void* xh, void* stream) {
-  EXL3_CHECK_ARG(x && topk_ids && suh && xh, "exl3_moe_had_in: null pointer");
+  EXL3_CHECK_ARG((tokens == 0 || (x && topk_ids && xh)) && suh, "exl3_moe_had_in: null pointer");
   EXL3_CHECK_ARG(shards == 1 || shards == 2, "exl3_moe_had_in: shards = %d (1 or 2)", shards);
   EXL3_CHECK_ARG(suh[0] && (shards == 1 || suh[1]), "exl3_moe_had_in: null suh");
   EXL3_CHECK_ARG(tokens >= 0 && top_k >= 1 && k > 0 && k % 128 == 0 && num_experts >= 1,
@@ -391,7 +391,8 @@ extern "C" int exl3_moe_gemm(const void* a, int rows, int k, const void* const* 
                              int shards, int n, const int* sorted_ids, const int* expert_ids,
                              const int* num_post_padded, int max_blocks, int block, int num_experts, int K,
                              int codebook, void* c, void* workspace, size_t workspace_bytes, void* stream) {
-  EXL3_CHECK_ARG(a && trellis && sorted_ids && expert_ids && num_post_padded && c, "exl3_moe_gemm: null pointer");
+  EXL3_CHECK_ARG((rows == 0 || (a && sorted_ids && expert_ids && num_post_padded && c)) && trellis,
+                 "exl3_moe_gemm: null pointer");
   EXL3_CHECK_ARG(shards == 1 || shards == 2, "exl3_moe_gemm: shards = %d (1 or 2)", shards);
   EXL3_CHECK_ARG(trellis[0] && (shards == 1 || trellis[1]), "exl3_moe_gemm: null trellis");
   EXL3_CHECK_ARG(!svh || (svh[0] && (shards == 1 || svh[1])), "exl3_moe_gemm: svh given with a null shard");
@@ -450,10 +451,10 @@ extern "C" int exl3_moe_gemm(const void* a, int rows, int k, const void* const* 
 
 extern "C" int exl3_moe_glu_had_in(const void* gu, int slots, int inter, const int* topk_ids, int num_experts,
                                    const void* suh_down, void* act, void* xd, void* stream) {
-  EXL3_CHECK_ARG(gu && topk_ids && suh_down && xd, "exl3_moe_glu_had_in: null pointer");
+  EXL3_CHECK_ARG((slots == 0 || (gu && topk_ids && xd)) && suh_down, "exl3_moe_glu_had_in: null pointer");
   EXL3_CHECK_ARG(slots >= 0 && inter > 0 && inter % 128 == 0 && num_experts >= 1,
                  "exl3_moe_glu_had_in: slots = %d, inter = %d, num_experts = %d", slots, inter, num_experts);
-  EXL3_CHECK_ARG(act != xd && act != gu, "exl3_moe_glu_had_in: act must not alias gu or xd");
+  EXL3_CHECK_ARG(slots == 0 || (act != xd && act != gu), "exl3_moe_glu_had_in: act must not alias gu or xd");
   EXL3_CHECK_ARG((int64_t)slots * 2 * inter <= INT32_MAX, "exl3_moe_glu_had_in: too many rows");
   if (slots == 0) return EXL3_OK;
   const dim3 grid((unsigned)(((int64_t)slots * (inter / 128) + 7) / 8));

@@ -397,7 +397,7 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
                                         const void* seq_lens, int batch, int num_q_heads, int num_kv_heads,
                                         int head_dim, int page_size, int bits, float sm_scale, void* out,
                                         void* workspace, size_t workspace_bytes, void* stream) {
-  EXL3_CHECK_ARG(q && k_cache && v_cache && k_scale && v_scale && page_table && seq_lens && out,
+  EXL3_CHECK_ARG((batch == 0 || (q && page_table && seq_lens && out)) && k_cache && v_cache && k_scale && v_scale,
                  "exl3_kv_decode_attention: null pointer");
   EXL3_CHECK_ARG(head_dim == kHeadDim && page_size == kPage,
                  "exl3_kv_decode_attention: head_dim = %d, page_size = %d (supported: 128, 16)", head_dim, page_size);
