@@ -136,6 +136,22 @@ def test_reported_workspace_sizes_cover_every_launch_plan(lib):
                         _lib.EXL3_ERR_INVALID, (K, k, n, rows)
 
 
+def test_kv_workspace_reserved_for_the_largest_batch_covers_every_smaller_call(lib):
+    """A smaller batch can split each sequence into more page chunks, so the KV workspace is not monotone in the
+    batch: the reservation takes the maximum over batch sizes 1..max_batch at the reserved page count, and that must
+    cover every call with fewer sequences or fewer pages (a captured graph keeps the reserved buffer)."""
+    for hkv, hq in ((1, 1), (2, 32), (4, 16), (8, 40), (8, 64)):
+        for max_batch in (1, 3, 16, 33):
+            for max_pages in (1, 7, 64, 256, 2048):
+                reserved = max(lib.exl3_kv_decode_workspace_bytes(b, hq, hkv, max_pages)
+                               for b in range(1, max_batch + 1))
+                for b in range(1, max_batch + 1):
+                    for p in sorted({1, 2, 5, 8, 9, 63, 100, max_pages // 2, max_pages - 1, max_pages}):
+                        if 1 <= p <= max_pages:
+                            need = lib.exl3_kv_decode_workspace_bytes(b, hq, hkv, p)
+                            assert 0 < need <= reserved, (hkv, hq, max_batch, max_pages, b, p)
+
+
 def test_zero_rows_launch_nothing_and_accept_null_data_pointers(lib):
     """Every entry point called with zero rows / tokens / slots / sequences returns EXL3_OK before any HIP call, with
     its activation, output and routing pointers NULL (weights and caches still given): an empty batch is a no-op,

@@ -123,7 +123,7 @@ def test_moe_graph_after_reservation():
     assert _ws_ptr("moe") == ptr
 
 
-@pytest.mark.parametrize("max_pages", [64, 4])   # 16 chunks and a merge launch / one chunk, no merge launch
+@pytest.mark.parametrize("max_pages", [64, 4])   # 8 chunks and a merge launch / one chunk, no merge launch
 def test_kv_graph_after_reservation(max_pages):
     ops = _ops()
     g = torch.Generator().manual_seed(61 + max_pages)

@@ -8,9 +8,9 @@
 //   page_table int32 [B][max_pages]; seq_lens int32 [B]; q fp16 [B][Hq][D]; out fp16 [B][Hq][D]; D = 128.
 //   Query head h reads KV head h / (Hq / Hkv).
 //
-// kv_decode_kernel: grid (chunks of chunk_pages pages, Hkv, B), 4 waves.  Wave w takes pages w, w+4, ... of its
-// workgroup's chunk, with the next page's codes in flight while it works on the current one, and keeps an online
-// softmax for the G = Hq/Hkv query heads (G <= 16; MFMA columns G..15 are idle).  Per 16-token page -- exactly one
+// kv_decode_kernel: grid (chunks of chunk_pages pages, Hkv, B), W = 8 (or 4) waves.  Wave w takes pages w, w+W, ...
+// of its workgroup's chunk, with the next page's codes in flight while it works on the current one, and keeps an
+// online softmax for the G = Hq/Hkv query heads (G <= 16; MFMA columns G..15 are idle).  Per 16-token page -- exactly one
 // 16-wide MFMA block, so the page's two scales are wave-uniform:
 //   S^T = K Q^T     4 x MFMA 16x16x32 f16.  A = the page's 16 keys (lane: key l%16, 32 dims), B = Q^T (lane: query
 //                   l%16, the same 32 dims in the same order; loaded once).  C lane: query l%16, keys 4(l/16)..+3;
@@ -21,7 +21,7 @@
 // Codes become fp16 without conversions: code + bias (bias 128 / 8, one xor) as the low byte (nibble) under 0x64 is
 // the fp16 1024 + bias + code.  V: one packed fp16 subtract of 1024 + bias leaves the code exactly (integers of
 // magnitude <= 128 are exact in fp16) before it is accumulated.  K: the MFMA takes the biased codes and the page's
-// logits subtract (1024 + bias) * sum(q) -- a per-page correction, never accumulated across pages.  The four waves
+// logits subtract (1024 + bias) * sum(q) -- a per-page correction, never accumulated across pages.  The W waves
 // merge their (m, l, O) in LDS; the workgroup writes its chunk's partial state and kv_merge_kernel combines the
 // chunks by log-sum-exp, in chunk order (deterministic).  Logits are kept in the base-2 domain (scale * log2 e).
 #include <math.h>
@@ -39,7 +39,8 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef uint32_t kv_u32x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t kv_u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kKvWaves = 4;
+constexpr int kKvWaves = 8;     // waves per decode workgroup (4 when the LDS merge of 8 would not fit 64 KB)
+constexpr int kMergeWaves = 4;  // waves per kv_merge_kernel workgroup
 constexpr int kHeadDim = 128;
 constexpr int kPage = 16;
 constexpr int kMaxGroup = 16;
@@ -204,15 +205,15 @@ struct KvState {
   }
 };
 
-template <int BITS, int DEPTH>
-__global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
+template <int BITS, int DEPTH, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void kv_decode_kernel(
     const _Float16* __restrict__ q, const uint8_t* kc, const uint8_t* vc, const _Float16* ksc, const _Float16* vsc,
     int num_pages,
     const int* __restrict__ page_table, int max_pages, const int* __restrict__ seq_lens, int Hq, int Hkv,
     float qk_scale, int chunk_pages, float* __restrict__ part_o, float* __restrict__ part_ml,
     _Float16* __restrict__ out) {
   constexpr int ROW = KvRegs<BITS>::ROW;
-  extern __shared__ float red[];  // [4 waves][G][D + 1] then [4 waves][G][2]
+  extern __shared__ float red[];  // [WAVES][G][D + 1] then [WAVES][G][2]
   const int chunk = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int G = Hq / Hkv;
   const int L = min(seq_lens[b], max_pages * kPage);
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
 #pragma unroll
   for (int db = 0; db < 8; db++) s.o[db] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  // this wave's pages: logical pages p0 + w, p0 + w + 4, ... below min(chunk end, pages of the sequence)
+  // this wave's pages: logical pages p0 + w, p0 + w + WAVES, ... below min(chunk end, pages of the sequence)
   const int p0 = chunk * chunk_pages;
   const int p_end = min(p0 + chunk_pages, (L + kPage - 1) / kPage);
   const int* ptab = page_table + (size_t)b * max_pages;
@@ -258,25 +259,25 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
       dst.load(kc + bi * blk_bytes, vc + bi * blk_bytes, ksc, vsc, bi, n, g);
     };
 #pragma unroll
-    for (int j = 0; j < DEPTH - 1; j++) load(r[j], lp + j * kKvWaves);
+    for (int j = 0; j < DEPTH - 1; j++) load(r[j], lp + j * WAVES);
     bool more = true;
     while (more) {
 #pragma unroll
       for (int j = 0; j < DEPTH; j++) {
         if (more) {
-          load(r[(j + DEPTH - 1) % DEPTH], lp + (DEPTH - 1) * kKvWaves);
+          load(r[(j + DEPTH - 1) % DEPTH], lp + (DEPTH - 1) * WAVES);
           issue_fence();
           s.process(r[j], qf, qsum, lp * kPage, L, qk_scale, g);
-          lp += kKvWaves;
+          lp += WAVES;
           more = lp < p_end;
         }
       }
     }
   }
 
-  // merge the 4 waves; lane (n, g) holds dims 32g + 8i + db (i < 4, db < 8) of query n
+  // merge the waves; lane (n, g) holds dims 32g + 8i + db (i < 4, db < 8) of query n
   float* red_o = red;
-  float* red_ml = red + kKvWaves * G * (kHeadDim + 1);
+  float* red_ml = red + WAVES * G * (kHeadDim + 1);
   if (n < G) {
     float* dst = red_o + (w * G + n) * (kHeadDim + 1) + 32 * g;
 #pragma unroll
@@ -293,10 +294,10 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
   if (tq >= G) return;
   float mx = -INFINITY;
 #pragma unroll
-  for (int ww = 0; ww < kKvWaves; ww++) mx = fmaxf(mx, red_ml[(ww * G + tq) * 2]);
+  for (int ww = 0; ww < WAVES; ww++) mx = fmaxf(mx, red_ml[(ww * G + tq) * 2]);
   float lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ww = 0; ww < kKvWaves; ww++) {
+  for (int ww = 0; ww < WAVES; ww++) {
     const float mw = red_ml[(ww * G + tq) * 2];
     const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
     lsum += red_ml[(ww * G + tq) * 2 + 1] * f;
@@ -323,18 +324,18 @@ __global__ __launch_bounds__(kKvWaves * 64) void kv_decode_kernel(
 
 // out[b][h] = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  One workgroup per query head; wave w folds chunks
 // w, w+4, ... into a running (M, L, O) (lane: dims 2l, 2l+1), then the 4 waves combine in LDS.  Fixed order.
-__global__ __launch_bounds__(256) void kv_merge_kernel(const float* __restrict__ part_o,
+__global__ __launch_bounds__(kMergeWaves * 64) void kv_merge_kernel(const float* __restrict__ part_o,
                                                        const float* __restrict__ part_ml, int Hq, int Hkv, int chunks,
                                                        _Float16* __restrict__ out) {
-  __shared__ float sm_ml[kKvWaves][2];
-  __shared__ float sm_o[kKvWaves][kHeadDim];
+  __shared__ float sm_ml[kMergeWaves][2];
+  __shared__ float sm_o[kMergeWaves][kHeadDim];
   const int h = blockIdx.x, b = blockIdx.y;
   const int G = Hq / Hkv, hk = h / G, q = h - hk * G;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63;
   const size_t base = ((size_t)b * Hkv + hk) * chunks;  // slot of chunk c: (base + c) * G + q
   float M = -INFINITY, L = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll 4
-  for (int c = w; c < chunks; c += kKvWaves) {
+  for (int c = w; c < chunks; c += kMergeWaves) {
     const size_t slot = (base + c) * G + q;
     const float mc = part_ml[slot * 2], lc = part_ml[slot * 2 + 1];
     const float2 oc = *reinterpret_cast<const float2*>(part_o + slot * kHeadDim + 2 * l);
@@ -358,10 +359,10 @@ __global__ __launch_bounds__(256) void kv_merge_kernel(const float* __restrict__
   const int d = threadIdx.x;
   float mx = -INFINITY;
 #pragma unroll
-  for (int ww = 0; ww < kKvWaves; ww++) mx = fmaxf(mx, sm_ml[ww][0]);
+  for (int ww = 0; ww < kMergeWaves; ww++) mx = fmaxf(mx, sm_ml[ww][0]);
   float lsum = 0.f, acc = 0.f;
 #pragma unroll
-  for (int ww = 0; ww < kKvWaves; ww++) {
+  for (int ww = 0; ww < kMergeWaves; ww++) {
     const float f = sm_ml[ww][0] == mx ? 1.f : __builtin_amdgcn_exp2f(sm_ml[ww][0] - mx);
     lsum += sm_ml[ww][1] * f;
     acc += sm_o[ww][d] * f;
@@ -369,15 +370,25 @@ __global__ __launch_bounds__(256) void kv_merge_kernel(const float* __restrict__
   out[((size_t)b * Hq + h) * kHeadDim + d] = (_Float16)(lsum > 0.f ? acc / lsum : 0.f);
 }
 
-// Pages per workgroup: the chunks of all (sequence, kv head) pairs should fill the GPU about `target` workgroups
-// deep (fewer chunks mean fewer partial states to write and merge); a multiple of the 4 waves.
-static int kv_chunk_pages(int batch, int num_kv_heads, int max_pages) {
-  int target = 1024;
+// Workgroup shape and pages per workgroup.  8 waves per workgroup and chunks that fill the GPU about one workgroup
+// per CU (256) deep; groups whose 8-wave LDS merge would pass 64 KB take 4 waves and about 1024 workgroups.  Fewer
+// chunks mean fewer partial states to write and merge: at 16 sequences x 8 kv heads, 2 chunks of 8 waves measured 3 %
+// faster (8-bit) than 8 chunks of 4 waves, and 4 chunks of 8 waves or 2 of 16 no faster than 2 of 8.  chunk_pages is
+// a multiple of the wave count.
+struct KvPlan {
+  int waves, chunk_pages, chunks;
+};
+static KvPlan kv_plan(int batch, int num_kv_heads, int group, int max_pages) {
+  int waves = kKvWaves;
+  if (const char* e = getenv("EXL3_KV_WAVES")) waves = atoi(e) == 4 ? 4 : kKvWaves;
+  if ((size_t)waves * group * (kHeadDim + 1 + 2) * sizeof(float) > 65536) waves = 4;
+  int target = waves == 8 ? 256 : 1024;
   if (const char* e = getenv("EXL3_KV_TARGET_WGS")) target = std::max(1, atoi(e));
   const long pairs = (long)batch * num_kv_heads;
-  const long chunks = std::max(1L, std::min((long)(max_pages + kKvWaves - 1) / kKvWaves, (target + pairs - 1) / pairs));
-  const int cp = (int)((max_pages + chunks - 1) / chunks);
-  return (cp + kKvWaves - 1) / kKvWaves * kKvWaves;
+  const long chunks = std::max(1L, std::min((long)(max_pages + waves - 1) / waves, (target + pairs - 1) / pairs));
+  int cp = (int)((max_pages + chunks - 1) / chunks);
+  cp = (cp + waves - 1) / waves * waves;
+  return KvPlan{waves, cp, (max_pages + cp - 1) / cp};
 }
 
 }  // namespace exl3
@@ -386,9 +397,9 @@ using namespace exl3;
 
 extern "C" size_t exl3_kv_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_pages) {
   if (batch <= 0 || num_kv_heads <= 0 || num_q_heads < num_kv_heads || max_pages <= 0) return 0;
-  const int cp = kv_chunk_pages(batch, num_kv_heads, max_pages);
-  const size_t chunks = (max_pages + cp - 1) / cp;
-  const size_t slots = (size_t)batch * num_kv_heads * chunks * (num_q_heads / num_kv_heads);
+  const int G = num_q_heads / num_kv_heads;
+  const KvPlan plan = kv_plan(batch, num_kv_heads, G, max_pages);
+  const size_t slots = (size_t)batch * num_kv_heads * plan.chunks * G;
   return slots * (kHeadDim + 2) * sizeof(float);
 }
 
@@ -412,12 +423,12 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
   EXL3_CHECK_ARG(workspace && workspace_bytes >= need, "exl3_kv_decode_attention: workspace %zu bytes, need %zu",
                  workspace_bytes, need);
   const int G = num_q_heads / num_kv_heads;
-  const int cp = kv_chunk_pages(batch, num_kv_heads, max_pages);
-  const int chunks = (max_pages + cp - 1) / cp;
+  const KvPlan plan = kv_plan(batch, num_kv_heads, G, max_pages);
+  const int chunks = plan.chunks;
   float* part_o = static_cast<float*>(workspace);
   float* part_ml = part_o + (size_t)batch * num_kv_heads * chunks * G * kHeadDim;
   const float qk_scale = sm_scale * 1.4426950408889634f;  // logits in base 2
-  const size_t lds = (size_t)kKvWaves * G * (kHeadDim + 1 + 2) * sizeof(float);
+  const size_t lds = (size_t)plan.waves * G * (kHeadDim + 1 + 2) * sizeof(float);
   hipStream_t st = as_stream(stream);
   const dim3 grid(chunks, num_kv_heads, batch);
   auto qp = static_cast<const _Float16*>(q);
@@ -429,17 +440,18 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
   auto sl = static_cast<const int*>(seq_lens);
   int depth = 2;  // register page sets per wave (prefetch distance + 1); deeper sets measured no faster
   if (const char* e = getenv("EXL3_KV_DEPTH")) depth = std::min(5, std::max(2, atoi(e)));
-  using Kern = decltype(&kv_decode_kernel<8, 2>);
-  static const Kern table[2][4] = {{kv_decode_kernel<4, 2>, kv_decode_kernel<4, 3>, kv_decode_kernel<4, 4>,
-                                    kv_decode_kernel<4, 5>},
-                                   {kv_decode_kernel<8, 2>, kv_decode_kernel<8, 3>, kv_decode_kernel<8, 4>,
-                                    kv_decode_kernel<8, 5>}};
-  table[bits == 8][depth - 2]<<<grid, kKvWaves * 64, lds, st>>>(qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl,
-                                                                num_q_heads, num_kv_heads, qk_scale, cp, part_o,
-                                                                part_ml, static_cast<_Float16*>(out));
+  using Kern = decltype(&kv_decode_kernel<8, 2, 4>);
+  static const Kern table[2][2][4] = {
+      {{kv_decode_kernel<4, 2, 4>, kv_decode_kernel<4, 3, 4>, kv_decode_kernel<4, 4, 4>, kv_decode_kernel<4, 5, 4>},
+       {kv_decode_kernel<8, 2, 4>, kv_decode_kernel<8, 3, 4>, kv_decode_kernel<8, 4, 4>, kv_decode_kernel<8, 5, 4>}},
+      {{kv_decode_kernel<4, 2, 8>, kv_decode_kernel<4, 3, 8>, kv_decode_kernel<4, 4, 8>, kv_decode_kernel<4, 5, 8>},
+       {kv_decode_kernel<8, 2, 8>, kv_decode_kernel<8, 3, 8>, kv_decode_kernel<8, 4, 8>, kv_decode_kernel<8, 5, 8>}}};
+  table[plan.waves == 8][bits == 8][depth - 2]<<<grid, plan.waves * 64, lds, st>>>(
+      qp, kp, vp, ksp, vsp, num_pages, pt, max_pages, sl, num_q_heads, num_kv_heads, qk_scale, plan.chunk_pages,
+      part_o, part_ml, static_cast<_Float16*>(out));
   EXL3_CHECK_LAUNCH();
   if (chunks > 1) {
-    kv_merge_kernel<<<dim3(num_q_heads, batch), 256, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
+    kv_merge_kernel<<<dim3(num_q_heads, batch), kMergeWaves * 64, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
                                                                static_cast<_Float16*>(out));
     EXL3_CHECK_LAUNCH();
   }

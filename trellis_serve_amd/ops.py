@@ -182,10 +182,13 @@ def reserve_moe_stage(device: torch.device, max_slots: int, k: int, n: int, shar
 
 
 def reserve_kv(device: torch.device, max_batch: int, num_q_heads: int, num_kv_heads: int, max_pages: int) -> None:
-    """Reserves the KV decode-attention workspace for batches of up to `max_batch` sequences of `max_pages` pages."""
+    """Reserves the KV decode-attention workspace for batches of up to `max_batch` sequences of up to `max_pages`
+    pages (a smaller batch can take more page chunks per sequence, so every batch size is sized; fewer pages never
+    need more)."""
     lib = _lib.load()
     dev = torch.device("cuda", _dev_index(device))
-    _ws("kv", dev).reserve(dev, lib.exl3_kv_decode_workspace_bytes(max_batch, num_q_heads, num_kv_heads, max_pages))
+    _ws("kv", dev).reserve(dev, _max_need(
+        lambda b: lib.exl3_kv_decode_workspace_bytes(b, num_q_heads, num_kv_heads, max_pages), max_batch))
 
 
 def reserve_workspace(device: torch.device, rows: int, k: int, n_total: int, K: int) -> None:
