@@ -215,8 +215,9 @@ __global__ __launch_bounds__(256) void had_out_kernel(const uint16_t* __restrict
 // straight-line (NT is a template parameter): no loop-carried load registers, exact in-order vmcnt waits.  A split
 // shorter than NT rows (the last one) clamps its loads to its last block and sees zero activations past its end.
 //
-// Every decoded tile feeds one MFMA 16x16x16 f16 on two alternating accumulators.  The prologue stages the split's
-// rotated activations (ROTATE) or the given ones into LDS in MFMA A order.
+// Every two decoded tiles (tile rows 2v and 2v + 1 of the wave's column) feed one MFMA 16x16x32 f16 per 16-row
+// group, on two alternating accumulators.  The prologue stages the split's rotated activations (ROTATE) or the given
+// ones into LDS in MFMA A order.
 //
 // Split-K epilogue (the slot reduce of cuda/csrc/exl3_marlin_template.h:2234-2262, in one launch): every split
 // writes its fp32 partial [split][m][col]; the last split of a column block to arrive (a per-block counter in the
