@@ -266,7 +266,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
   const int kb0 = split * NB;
   const int nb = min(k >> 7, kb0 + NB) - kb0;  // blocks of this split holding data (1..NB)
   constexpr int mstride = a_mstride(NT);
-  auto stage1 = [&](int p, int m, _Float16 h) { xs[a_slot(p, m, mstride)] = h; };  // one activation value
+  // four consecutive activations p .. p+3 (p a multiple of 4): a_slot keeps each even-odd pair adjacent
+  auto stage4 = [&](int p, int m, const _Float16 (&h)[4]) {
+    *reinterpret_cast<half2_t*>(xs + a_slot(p, m, mstride)) = half2_t{h[0], h[1]};
+    *reinterpret_cast<half2_t*>(xs + a_slot(p + 2, m, mstride)) = half2_t{h[2], h[3]};
+  };
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, c = l & 15, j = l >> 4;
@@ -334,8 +338,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
           h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
         }
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) stage1(b * 128 + 4 * t + i, m, h[i]);
+      stage4(b * 128 + 4 * t, m, h);
     }
   } else {
     for (int u = hw; u < Mp * NB; u += 2 * kGemvWaves) {
@@ -353,8 +356,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(ShardArgs sa, const 
           h[0] = v.x; h[1] = v.y; h[2] = v.z; h[3] = v.w;
         }
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) stage1(b * 128 + 4 * t + i, m, h[i]);
+      stage4(b * 128 + 4 * t, m, h);
     }
   }
   __syncthreads();

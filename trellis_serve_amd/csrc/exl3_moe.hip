@@ -387,8 +387,9 @@ __global__ __launch_bounds__(kMoeThreads, (PRE && P <= 2 && K <= 4) ? 8 : 1) voi
             else
               moe_glu4(a, gu, suh, slot_at(c0 + m), (kb0 + b) * 128 + 4 * t, h);
           }
-#pragma unroll
-          for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, mstride)] = h[i];
+          // a_slot keeps each even-odd pair of positions adjacent: two 4-byte writes
+          *reinterpret_cast<half2_t*>(xs + a_slot(b * 128 + 4 * t, m, mstride)) = half2_t{h[0], h[1]};
+          *reinterpret_cast<half2_t*>(xs + a_slot(b * 128 + 4 * t + 2, m, mstride)) = half2_t{h[2], h[3]};
         }
         __syncthreads();
         // A row of lane group c in group p: 16 p + c (group 0: min(c, M - 1)); rows >= M feed only C rows never stored

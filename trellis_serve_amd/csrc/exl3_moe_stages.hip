@@ -208,8 +208,9 @@ __global__ __launch_bounds__(kStageThreads) void moe_block_gemm_kernel(
         const int r = ids[m];
         if (r < rows) v = *reinterpret_cast<const half4_t*>(arows + (size_t)r * k + (kb0 + b) * 128 + 4 * t);
       }
-#pragma unroll
-      for (int i = 0; i < 4; i++) xs[a_slot(b * 128 + 4 * t + i, m, kStageMStride)] = v[i];
+      // a_slot keeps each even-odd pair of positions adjacent: two 4-byte writes
+      *reinterpret_cast<half2_t*>(xs + a_slot(b * 128 + 4 * t, m, kStageMStride)) = half2_t{v[0], v[1]};
+      *reinterpret_cast<half2_t*>(xs + a_slot(b * 128 + 4 * t + 2, m, kStageMStride)) = half2_t{v[2], v[3]};
     }
     __syncthreads();
     stream.template run_groups<P>(reinterpret_cast<const half8_t*>(xs + cl * kStageMStride) + j,
