@@ -10,8 +10,8 @@
 //
 // kv_decode_kernel: grid (chunks of chunk_pages pages, Hkv, B), W = 8 (or 4) waves.  Wave w takes pages w, w+W, ...
 // of its workgroup's chunk, with the next page's codes in flight while it works on the current one, and keeps an
-// online softmax for the G = Hq/Hkv query heads (G <= 16; MFMA columns G..15 are idle).  Per 16-token page -- exactly one
-// 16-wide MFMA block, so the page's two scales are wave-uniform:
+// online softmax for the G = Hq/Hkv query heads (G <= 16; MFMA columns G..15 are idle).  Per 16-token page --
+// exactly one 16-wide MFMA block, so the page's two scales are wave-uniform:
 //   S^T = K Q^T     4 x MFMA 16x16x32 f16.  A = the page's 16 keys (lane: key l%16, 32 dims), B = Q^T (lane: query
 //                   l%16, the same 32 dims in the same order; loaded once).  C lane: query l%16, keys 4(l/16)..+3;
 //   P^T             that C layout is already the B operand of the next MFMA; P' = p * v_scale rounded to fp16;
@@ -451,8 +451,9 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
       part_o, part_ml, static_cast<_Float16*>(out));
   EXL3_CHECK_LAUNCH();
   if (chunks > 1) {
-    kv_merge_kernel<<<dim3(num_q_heads, batch), kMergeWaves * 64, 0, st>>>(part_o, part_ml, num_q_heads, num_kv_heads, chunks,
-                                                               static_cast<_Float16*>(out));
+    kv_merge_kernel<<<dim3(num_q_heads, batch), kMergeWaves * 64, 0, st>>>(part_o, part_ml, num_q_heads,
+                                                                           num_kv_heads, chunks,
+                                                                           static_cast<_Float16*>(out));
     EXL3_CHECK_LAUNCH();
   }
   return EXL3_OK;
