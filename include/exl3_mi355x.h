@@ -281,7 +281,8 @@ int exl3_moe_combine(const void* yd, const float* topk_weights, const int* topk_
  * [num_pages][Hkv][16][64] (bits = 4: element 2i in the low nibble, 2i+1 in the high nibble, two's complement);
  * k_scale / v_scale fp16 [num_pages][Hkv]; value = code * scale. */
 
-/* Workspace bytes of exl3_kv_decode_attention (fp32 partial (m, l, O) per chunk of pages).  No zero-fill needed. */
+/* Workspace bytes of exl3_kv_decode_attention (fp32 partial (m, l, O) per chunk of pages).  No zero-fill needed.
+ * Not monotone in batch (a smaller batch can take more chunks per sequence); never larger for fewer pages. */
 size_t exl3_kv_decode_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_pages);
 /* out[b][h] = softmax(sm_scale * q[b][h] . K_b^T) V_b over the first seq_lens[b] tokens of sequence b, whose pages are
  * page_table[b][0 .. ceil(seq_lens[b] / 16)); query head h reads KV head h / (Hq / Hkv) (Hq / Hkv <= 16).
