@@ -565,8 +565,10 @@ def _under_profiler() -> bool:
 
 def probe(kind: str, launches: int) -> int:
     """Short GPU programs for counter passes: `gate_up` launches the dominant GEMV kernel `launches` times over five
-    rotating copies of the layer; `prefill` the configs[2] decode-GEMM (5120 -> 17408, K = 3 MCG, M = 2048); `copy` runs a plain
-    512 MiB device copy (the calibration of FETCH_SIZE / WRITE_SIZE)."""
+    rotating copies of the layer; `prefill` the configs[2] decode-GEMM (5120 -> 17408, K = 3 MCG, M = 2048); `kv8` /
+    `kv4` the configs[4] KV decode attention at 4k context (B = 16, 40 / 8 heads, 8- / 4-bit codes, four rotating
+    caches in a random page order); `copy` runs a plain 512 MiB device copy (the calibration of FETCH_SIZE /
+    WRITE_SIZE)."""
     import torch
 
     from trellis_serve_amd import ops
@@ -580,6 +582,20 @@ def probe(kind: str, launches: int) -> int:
         y = ops.linear_prefill(x, [tr], [suh], [svh], CODEBOOK)
         for _ in range(launches):
             ops.linear_prefill(x, [tr], [suh], [svh], CODEBOOK, out=y)
+    elif kind in ("kv8", "kv4"):
+        bits, B, Hq, Hkv, D, L = int(kind[2:]), 16, 40, 8, 128, 4096
+        g = torch.Generator(device="cpu").manual_seed(13)
+        P, row = B * L // 16, D if bits == 8 else D // 2
+        sets = [(torch.randint(-128, 128, (P, Hkv, 16, row), dtype=torch.int8, device=dev),
+                 torch.randint(-128, 128, (P, Hkv, 16, row), dtype=torch.int8, device=dev),
+                 (torch.rand((P, Hkv), device=dev) * 0.02 + 0.01).half(),
+                 (torch.rand((P, Hkv), device=dev) * 0.02 + 0.01).half(),
+                 torch.randperm(P, generator=g).to(torch.int32).view(B, L // 16).to(dev)) for _ in range(4)]
+        q = torch.randn((B, Hq, D), generator=g).half().to(dev)
+        lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+        o = torch.empty((B, Hq, D), dtype=torch.float16, device=dev)
+        for i in range(launches):
+            ops.kv_decode_attention(q, *sets[i % 4][:4], sets[i % 4][4], lens, bits, out=o)
     elif kind == "copy":
         src = torch.empty(128 << 20, dtype=torch.float32, device=dev).uniform_()
         dst = torch.empty_like(src)
@@ -652,7 +668,7 @@ def main() -> int:
                     help="also report these M (comma list, '' for none; past 16 rows the GEMV takes 2 or 4 row groups)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-secondary", action="store_true", help="skip the prefill / MoE / KV-attention lines")
-    ap.add_argument("--probe", choices=["gate_up", "prefill", "copy"], help=argparse.SUPPRESS)
+    ap.add_argument("--probe", choices=["gate_up", "prefill", "kv8", "kv4", "copy"], help=argparse.SUPPRESS)
     ap.add_argument("--probe-launches", type=int, default=20, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.probe:
