@@ -94,19 +94,16 @@ struct KvRegs {
   static constexpr int KW = BITS == 8 ? 8 : 4;                      // K dwords per lane
   static constexpr int VW = BITS == 8 ? 8 : 4;                      // V dwords per lane
   uint32_t k[KW], v[VW];
-  uint32_t ksw, vsw;  // the aligned dwords holding the block's two fp16 scales (at bit ssh)
-  int ssh;
+  uint32_t ksw, vsw;  // the block's two fp16 scales, each zero-extended in a register of its own
 
   // lane (n, g): K row n, bytes [ROW/4 * g, +ROW/4); V rows 4g .. 4g+3, bytes [ROW/16 * n, +ROW/16)
-  __device__ __forceinline__ void load(const uint8_t* kblk, const uint8_t* vblk, const uint32_t* ksc,
-                                       const uint32_t* vsc, size_t bi, int n, int g) {
-    // The scales first, each as the aligned dword that holds it, into registers nothing copies before the scales
-    // are used: a 2-byte load gets packed (a copy that must wait for it), and as the youngest load of the page its
-    // wait would cover every load in flight.  A naturally aligned dword never crosses a page, so the half past the
-    // last scale of an odd-sized array reads mapped memory.
-    ksw = ksc[bi >> 1];
-    vsw = vsc[bi >> 1];
-    ssh = (int)(bi & 1) * 16;
+  __device__ __forceinline__ void load(const uint8_t* kblk, const uint8_t* vblk, const uint16_t* ksc,
+                                       const uint16_t* vsc, size_t bi, int n, int g) {
+    // The scales first, each zero-extended into a 32-bit register that nothing copies or packs before the scales are
+    // used: packed as fp16 halves of one register (a copy that must wait for both loads), and issued as the page's
+    // youngest loads, their wait covered every load in flight.
+    ksw = ksc[bi];
+    vsw = vsc[bi];
     const kv_u32x4_t* kp = reinterpret_cast<const kv_u32x4_t*>(kblk + n * ROW + (ROW / 4) * g);
     if constexpr (BITS == 8) {
       const kv_u32x4_t a = kp[0], b = kp[1];
@@ -123,8 +120,8 @@ struct KvRegs {
       for (int i = 0; i < 4; i++) v[i] = *reinterpret_cast<const uint32_t*>(vblk + (4 * g + i) * ROW + 4 * n);
     }
   }
-  __device__ __forceinline__ _Float16 kscale() const { return __builtin_bit_cast(_Float16, (uint16_t)(ksw >> ssh)); }
-  __device__ __forceinline__ _Float16 vscale() const { return __builtin_bit_cast(_Float16, (uint16_t)(vsw >> ssh)); }
+  __device__ __forceinline__ _Float16 kscale() const { return __builtin_bit_cast(_Float16, (uint16_t)ksw); }
+  __device__ __forceinline__ _Float16 vscale() const { return __builtin_bit_cast(_Float16, (uint16_t)vsw); }
 
   // K fragment c, biased: 1024 + bias + code (bias 128 / 8; removed after the MFMA, per page, from the query sums).
   // Dims of lane group g, in the order the Q fragment uses: 8 bits, dwords 2c, 2c+1 = dims 32g + 8c + 0..7;
@@ -215,7 +212,7 @@ struct KvState {
 
 template <int BITS, int DEPTH, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void kv_decode_kernel(
-    const _Float16* __restrict__ q, const uint8_t* kc, const uint8_t* vc, const uint32_t* ksc, const uint32_t* vsc,
+    const _Float16* __restrict__ q, const uint8_t* kc, const uint8_t* vc, const uint16_t* ksc, const uint16_t* vsc,
     int num_pages,
     const int* __restrict__ page_table, int max_pages, const int* __restrict__ seq_lens, int Hq, int Hkv,
     float qk_scale, int chunk_pages, float* __restrict__ part_o, float* __restrict__ part_ml,
@@ -442,8 +439,8 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
   auto qp = static_cast<const _Float16*>(q);
   auto kp = static_cast<const uint8_t*>(k_cache);
   auto vp = static_cast<const uint8_t*>(v_cache);
-  auto ksp = static_cast<const uint32_t*>(k_scale);  // fp16 pairs, read as the aligned dword holding a scale
-  auto vsp = static_cast<const uint32_t*>(v_scale);
+  auto ksp = static_cast<const uint16_t*>(k_scale);  // fp16 bits
+  auto vsp = static_cast<const uint16_t*>(v_scale);
   auto pt = static_cast<const int*>(page_table);
   auto sl = static_cast<const int*>(seq_lens);
   int depth = 2;  // register page sets per wave (prefetch distance + 1); deeper sets measured no faster
