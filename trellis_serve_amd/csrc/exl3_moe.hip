@@ -149,9 +149,18 @@ __device__ void moe_route_block(const int* __restrict__ topk_ids, int slots, int
   const int tid = threadIdx.x;
   for (int e = tid; e < 1024; e += 256) cnt[e] = 0;
   __syncthreads();
-  for (int s = tid; s < slots; s += 256) {
-    const int e = topk_ids[s];
-    if (e >= 0 && e < E) lists[(size_t)e * slots + atomicAdd(&cnt[e], 1)] = s;
+  // up to 8 ids per thread loaded together (2048 slots at 256 tokens: one load round trip instead of 8 in a chain);
+  // a slot's place in its expert's list follows the LDS atomics, and no result depends on it (every slot is its own
+  // row of the expert GEMVs)
+  for (int s0 = tid; s0 < slots; s0 += 256 * 8) {
+    int ev[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) ev[i] = s0 + 256 * i < slots ? topk_ids[s0 + 256 * i] : -1;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int e = ev[i];
+      if (e >= 0 && e < E) lists[(size_t)e * slots + atomicAdd(&cnt[e], 1)] = s0 + 256 * i;
+    }
   }
   __syncthreads();
   bool f[4];
