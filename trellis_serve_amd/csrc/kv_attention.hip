@@ -383,12 +383,20 @@ __global__ __launch_bounds__(kMergeWaves * 64) void kv_merge_kernel(const float*
 struct KvPlan {
   int waves, chunk_pages, chunks;
 };
+// EXL3_KV_WAVES (4 or 8) and EXL3_KV_TARGET_WGS override the plan for measurements; read once per process, so the
+// workspace size and the launch always follow the same plan.
 static KvPlan kv_plan(int batch, int num_kv_heads, int group, int max_pages) {
-  int waves = kKvWaves;
-  if (const char* e = getenv("EXL3_KV_WAVES")) waves = atoi(e) == 4 ? 4 : kKvWaves;
+  static const int env_waves = [] {
+    const char* e = getenv("EXL3_KV_WAVES");
+    return e && atoi(e) == 4 ? 4 : kKvWaves;
+  }();
+  static const int env_target = [] {
+    const char* e = getenv("EXL3_KV_TARGET_WGS");
+    return e ? std::max(1, atoi(e)) : 0;
+  }();
+  int waves = env_waves;
   if ((size_t)waves * group * (kHeadDim + 1 + 2) * sizeof(float) > 65536) waves = 4;
-  int target = waves == 8 ? 256 : 1024;
-  if (const char* e = getenv("EXL3_KV_TARGET_WGS")) target = std::max(1, atoi(e));
+  const int target = env_target ? env_target : waves == 8 ? 256 : 1024;
   const long pairs = (long)batch * num_kv_heads;
   const long chunks = std::max(1L, std::min((long)(max_pages + waves - 1) / waves, (target + pairs - 1) / pairs));
   int cp = (int)((max_pages + chunks - 1) / chunks);
@@ -443,8 +451,10 @@ extern "C" int exl3_kv_decode_attention(const void* q, const void* k_cache, cons
   auto vsp = static_cast<const uint16_t*>(v_scale);
   auto pt = static_cast<const int*>(page_table);
   auto sl = static_cast<const int*>(seq_lens);
-  int depth = 2;  // register page sets per wave (prefetch distance + 1); deeper sets measured no faster
-  if (const char* e = getenv("EXL3_KV_DEPTH")) depth = std::min(5, std::max(2, atoi(e)));
+  static const int depth = [] {  // register page sets per wave (prefetch distance + 1); deeper sets measured no faster
+    const char* e = getenv("EXL3_KV_DEPTH");
+    return e ? std::min(5, std::max(2, atoi(e))) : 2;
+  }();
   using Kern = decltype(&kv_decode_kernel<8, 2, 4>);
   static const Kern table[2][2][4] = {
       {{kv_decode_kernel<4, 2, 4>, kv_decode_kernel<4, 3, 4>, kv_decode_kernel<4, 4, 4>, kv_decode_kernel<4, 5, 4>},
