@@ -216,6 +216,33 @@ def test_one_group_split_plan_fills_its_last_round(lib):
             assert lib.exl3_linear_workspace_bytes(rows, k, n, 3) == want, (k, n, rows)
 
 
+def test_kv_chunk_plan_aims_at_one_workgroup_per_cu(lib):
+    """The KV decode plan, read back through the reported workspace size (batch x kv heads x chunks x group query
+    heads x (128 + 2) fp32): 8-wave workgroups and about 256 of them (one per CU), or 4 waves and about 1024 when the
+    8-wave LDS merge of the group would pass 64 KB (16-head groups); chunk pages a multiple of the wave count.  At the
+    measured configuration (16 sequences, 40 / 8 heads) that is 2 chunks at 4k and 32k.  A plan derived here
+    independently of the library."""
+    def chunks(batch, hq, hkv, max_pages):
+        g = hq // hkv
+        waves = 8 if 8 * g * 131 * 4 <= 65536 else 4
+        target = 256 if waves == 8 else 1024
+        pairs = batch * hkv
+        want = max(1, min(-(-max_pages // waves), -(-target // pairs)))
+        cp = -(-max_pages // want)
+        cp = -(-cp // waves) * waves
+        return -(-max_pages // cp)
+
+    assert chunks(16, 40, 8, 256) == 2 and chunks(16, 40, 8, 2048) == 2
+    assert chunks(1, 64, 4, 2048) == 256 and chunks(64, 32, 8, 100) == 1   # 16-head groups: 4 waves, ~1024
+    for batch in (1, 2, 5, 16, 33, 128):
+        for hq, hkv in ((8, 8), (40, 8), (60, 4), (32, 2), (64, 4), (16, 1)):
+            for max_pages in (1, 7, 8, 9, 64, 256, 1000, 2048):
+                g = hq // hkv
+                want = batch * hkv * chunks(batch, hq, hkv, max_pages) * g * 130 * 4
+                assert lib.exl3_kv_decode_workspace_bytes(batch, hq, hkv, max_pages) == want, \
+                    (batch, hq, hkv, max_pages)
+
+
 def test_mixed_moe_entry_points_reject_bad_class_counts(lib):
     P, I = ctypes.c_void_p, ctypes.c_int
     maps, blocks = (P * 3)(1, 1, 1), (I * 3)(16, 16, 16)
