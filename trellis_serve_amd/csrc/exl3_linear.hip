@@ -479,12 +479,15 @@ constexpr int kGemvOneGroupWgs = 448;
 // one-group workgroups resident at once on MI355X: 256 CUs x 4 (8 waves of <= 64 VGPRs, < 40 KB of LDS each).  A
 // constant, so that the plan (and with it every workspace size) depends on the arguments alone.
 constexpr int kGemvOneGroupSlots = 256 * 4;
-static int gemv_target_wgs() {
+// rows: the launch's rows (17-32: two row groups, 33-64: four).  Two-group launches aim at 512: q/k/v at 24-32 rows
+// then takes 32 tile rows (640 workgroups) instead of 16 (1280), 1-1.7 us less per step, and no other layer of the
+// layer set moves; four-group launches keep 768 (q/k/v at 48-64 rows 3 us slower at 512).
+static int gemv_target_wgs(int rows = kGemvQuadRows) {
   static const int env = [] {
     const char* e = getenv("EXL3_GEMV_TARGET_WGS");
     return e ? std::max(1, atoi(e)) : 0;
   }();
-  return env ? env : 768;
+  return env ? env : rows <= kGemvPairRows ? 512 : 768;
 }
 
 // pre: prepared rows (gemv_kernel<.., PRE>), whose 64-row-tile instance needs 132 VGPRs: at most 32 there.
@@ -528,7 +531,7 @@ static GemvPlan gemv_plan(int k, int n_total, int M, int K, bool pre = false) {
   for (int cand : {64, 32}) {
     const int splits = (kb + cand / 8 - 1) / (cand / 8);
     if (pre && cand > 32) continue;
-    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs() && gemv_lds_bytes(Ms, cand, K) <= kGemvMaxLds) {
+    if ((size_t)nblk * splits >= (size_t)gemv_target_wgs(M) && gemv_lds_bytes(Ms, cand, K) <= kGemvMaxLds) {
       nt = cand;
       break;
     }
